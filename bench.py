@@ -1,0 +1,227 @@
+"""Benchmark of one decode step of the paged tree-decode attention path.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu]
+
+A step is one dh_decode_batch call (attention items + log-sum-exp merge) over
+the workload's whole batch, with pages, queries and plans resident in HBM.
+The default workload is c3, the Llama-3-8B-shape 64-leaf MCTS tree the
+headline metric is quoted on.  To keep the 256 MB last-level cache from
+serving repeats, the step rotates over several copies of the tree on disjoint
+pages (more bytes than that cache holds).
+
+Prints one JSON line (rank 0).  value = algorithmic bytes / step time, in GB/s
+(algorithmic bytes: each referenced page's valid K/V bytes once, plus scale
+bytes, q and out).  roofline: the attention-item kernel alone, timed with HIP
+events on the stream it runs on, against the 8 TB/s HBM peak.  cpu_baseline:
+the C restatement of ReferenceBackend::decode (candle op order, f32,
+materialised gather/tile) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn achieved HBM GB/s (% of peak) + µs/step, 64-leaf 8B-shape tree"
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_workloads(name: str, rotations: int):
+    from dendrite_amd import workloads
+    if name == "c3":
+        per = workloads.c3().meta["pages_per_tree"]
+        rotations = max(1, min(rotations, 65536 // per))
+        return [workloads.c3(rotation=r) for r in range(rotations)]
+    return [workloads.ALL[name]()]
+
+
+def cpu_baseline(w, budget_s: float = 12.0):
+    """Times the oracle's candle-order f32 decode on a sample of sequences,
+    first one thread, then all host cores; scales to a full step."""
+    import oracle
+    ids = w.page_ids()
+    data, scales = w.make_pages(ids)
+    pv = oracle.PoolView(ids, data, scales, w.num_pool_pages, w.kv_format, w.hkv, w.d)
+    q = w.make_q()
+    cfg = w.attention_config()
+    mode = "candle" if w.name in ("c1", "c2", "c3") else "stream"
+    threads = oracle.lib().oracle_num_threads()
+    res = {}
+    for nthr in (1, threads):
+        seqs, t_used = [], 0.0
+        order = np.random.Generator(np.random.PCG64(7)).permutation(w.batch)
+        for b in order:
+            t0 = time.perf_counter()
+            oracle.decode(pv, q, w.q_dtype, w.hq, cfg.scale, w.gqa_mapping, w.indptr, w.indices,
+                          w.last_page_len, seqs=[int(b)] * max(1, nthr), threads=nthr, mode=mode)
+            dt = time.perf_counter() - t0
+            seqs.append(int(b))
+            t_used += dt
+            if t_used > budget_s / 2:
+                break
+        # each call ran nthr copies of one sequence in parallel
+        per_seq = t_used / (len(seqs) * max(1, nthr))
+        step_s = per_seq * w.batch
+        res[nthr] = (step_s, len(seqs) * max(1, nthr))
+    step_s, nsample = res[threads]
+    step1, n1 = res[1]
+    return {
+        "value": round(w.algorithmic_bytes() / step_s / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "us_per_step": round(step_s * 1e6, 1),
+        "sample": f"{nsample} sequence decodes of {w.name} ({mode} f32, OpenMP over sequences) "
+                  f"scaled to the {w.batch}-sequence step",
+        "one_thread": {"value": round(w.algorithmic_bytes() / step1 / 1e9, 4), "unit": "GB/s",
+                       "us_per_step": round(step1 * 1e6, 1), "sample": f"{n1} sequence decodes"},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c3")
+    ap.add_argument("--rotations", type=int, default=6)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--shared-chunk", type=int, default=0)
+    ap.add_argument("--private-chunk", type=int, default=0)
+    ap.add_argument("--target-items", type=int, default=0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path "
+                                   "shards by tree / KV head across GPUs, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    from dendrite_amd.backend import Backend, DecodePlan, Pool, decode_batch, raw_to_tensor
+
+    ws_list = build_workloads(args.workload, args.rotations)
+    w0 = ws_list[0]
+    log(f"[bench] workload {w0.name}: {w0.description}; {len(ws_list)} rotation(s)")
+    be = Backend(0)
+    pool = Pool(be, w0.num_pool_pages, w0.hkv, w0.d, w0.kv_format)
+    plans, qs, outs, lpls = [], [], [], []
+    for w in ws_list:
+        ids = w.page_ids()
+        data, scales = w.make_pages(ids)
+        pool.write_pages(ids, data, scales)
+        del data, scales
+        plan = DecodePlan(be, w.attention_config(), pool, w.indptr, w.indices, cascade=True,
+                          shared_chunk_pages=args.shared_chunk,
+                          private_chunk_pages=args.private_chunk, target_items=args.target_items)
+        plans.append(plan)
+        q = raw_to_tensor(w.make_q(), w.q_dtype)
+        qs.append(q)
+        outs.append(torch.empty_like(q))
+        lpls.append(torch.from_numpy(np.ascontiguousarray(w.last_page_len)).cuda())
+    ws = torch.empty(max(p.workspace_size for p in plans) + 256, dtype=torch.uint8, device="cuda")
+    st = plans[0].stats()
+    log(f"[bench] plan: {st}")
+    alg = w0.algorithmic_bytes()
+    alg_attend = alg - w0.batch * w0.hq * w0.d * (4 if w0.q_dtype == 2 else 2)   # no O writes
+    stream = torch.cuda.current_stream()
+    R = len(plans)
+
+    def step(i, stages=3):
+        k = i % R
+        decode_batch(plans[k], qs[k], outs[k], ws, lpls[k], stream=stream, stages=stages)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    def timed(stages):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for i in range(args.steps):
+            step(i, stages)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / args.steps
+
+    ms_step = timed(3)
+    ms_attend = timed(1)
+    ms_merge = timed(2)
+    # per-step distribution (single-step event pairs)
+    per = []
+    for i in range(min(args.steps, 100)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        step(i)
+        e1.record(stream)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1))
+    per = np.array(per)
+    log(f"[bench] step {ms_step * 1e3:.2f} us (attend {ms_attend * 1e3:.2f} us, merge {ms_merge * 1e3:.2f} us)"
+        f"; single-step median {np.median(per) * 1e3:.2f} us")
+
+    gbs = alg / (ms_step * 1e-3) / 1e9
+    attend_gbs = alg_attend / (ms_attend * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_step": round(ms_step * 1e3, 3),
+        "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "tokens_per_s": round(w0.batch / (ms_step * 1e-3), 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {1: "bf16", 0: "f16", 2: "f32"}[w0.q_dtype] +
+                 ({3: "+fp8e4m3-kv", 4: "+mxfp8-kv"}.get(w0.kv_format, "")),
+        "data": "synthetic (seeded N(0,1) K/V/q; tree shape per config)",
+        "config": {
+            "workload": f"{w0.name}: {w0.description}",
+            "leaves": w0.batch, "num_heads": w0.hq, "num_kv_heads": w0.hkv, "head_dim": w0.d,
+            "algorithmic_bytes_per_step": alg, "flops_per_step": w0.flops(),
+            "unique_pages": st["unique_pages"], "page_reads_per_kv_head": st["page_reads"],
+            "naive_kv_bytes": w0.naive_kv_bytes(), "rotations": R, "plan_items": st["num_items"],
+            "partials_per_row": st["num_partials"] / max(1, w0.batch),
+        },
+        "single_step_us": {"p10": round(float(np.percentile(per, 10)) * 1e3, 2),
+                           "median": round(float(np.median(per)) * 1e3, 2),
+                           "p90": round(float(np.percentile(per, 90)) * 1e3, 2)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attend16_kernel (attention items)",
+            "achieved": round(attend_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(attend_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(ms_attend * 1e3, 3),
+            "merge_launch_us": round(ms_merge * 1e3, 3),
+            "mfma_tflops": round(w0.flops() / (ms_attend * 1e-3) / 1e12, 2),
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(w0)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,352 @@
+"""Python host side of the HIP decode path, over the C ABI.
+
+  AttentionConfig  crates/dendrite-core/src/attention/backend.rs:17-59
+  HipBackend       the AttentionBackend trait (backend.rs:61-97) for the
+                   FlashInferBackend slot (attention/flashinfer.rs:211-269)
+  Pool / DecodePlan / decode_batch
+                   the raw C ABI (device page pool, decode plan, one step) that
+                   replaces dendrite-ffi's BatchDecodeKernel / CascadeAttention
+                   (crates/dendrite-ffi/src/flashinfer/{batch_decode,cascade}.rs)
+
+torch is used only to hold device memory and streams.  Every computation runs
+in libdendrite_hip.so; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import DhError, check, lib
+from .cache import BlockTable
+
+
+def _torch():
+    import torch  # noqa: PLC0415 — plumbing only, imported on first device use
+    return torch
+
+
+def dtype_code(t) -> int:
+    torch = _torch()
+    return {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
+            torch.float32: _lib.DTYPE_F32}[t]
+
+
+def torch_dtype(code: int):
+    torch = _torch()
+    return {_lib.DTYPE_F16: torch.float16, _lib.DTYPE_BF16: torch.bfloat16,
+            _lib.DTYPE_F32: torch.float32}[code]
+
+
+def raw_to_tensor(raw: np.ndarray, q_dtype: int, device: str = "cuda:0"):
+    """Device tensor from raw host bits (uint16 for f16/bf16, float32)."""
+    torch = _torch()
+    raw = np.ascontiguousarray(raw)
+    if q_dtype == _lib.DTYPE_F32:
+        return torch.from_numpy(raw.view(np.float32)).to(device)
+    t = torch.from_numpy(raw.view(np.int16))
+    return t.view(torch.bfloat16 if q_dtype == _lib.DTYPE_BF16 else torch.float16).to(device)
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    if stream is None:
+        torch = _torch()
+        return torch.cuda.current_stream().cuda_stream
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
+class AttentionConfig:
+    """AttentionConfig (backend.rs:17-59) plus the GQA mapping and dtypes."""
+
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int):
+        c = _lib.dh_attn_config()
+        check(lib().dh_attn_config_init(C.byref(c), num_heads, num_kv_heads, head_dim))
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.scale = float(c.scale)               # 1/sqrt(head_dim) in f32 (backend.rs:37)
+        self.sliding_window: Optional[int] = None
+        self.gqa_mapping = _lib.GQA_TILED         # ReferenceBackend's Tensor::repeat
+        self.q_dtype = _lib.DTYPE_BF16
+        self.kv_format = _lib.KV_BF16
+
+    @classmethod
+    def new(cls, num_heads: int, num_kv_heads: int, head_dim: int) -> "AttentionConfig":
+        return cls(num_heads, num_kv_heads, head_dim)
+
+    @classmethod
+    def default(cls) -> "AttentionConfig":        # backend.rs:54-58
+        return cls(8, 8, 64)
+
+    def with_sliding_window(self, window: int) -> "AttentionConfig":
+        self.sliding_window = window
+        return self
+
+    def num_queries_per_kv(self) -> int:
+        return self.num_heads // self.num_kv_heads
+
+    def to_c(self) -> _lib.dh_attn_config:
+        c = _lib.dh_attn_config()
+        c.num_heads, c.num_kv_heads, c.head_dim = self.num_heads, self.num_kv_heads, self.head_dim
+        c.scale = self.scale
+        c.sliding_window = self.sliding_window or 0
+        c.gqa_mapping = self.gqa_mapping
+        c.q_dtype = self.q_dtype
+        c.kv_format = self.kv_format
+        return c
+
+
+class Backend:
+    """dh_backend: one HIP device."""
+
+    def __init__(self, device: int = 0):
+        self._h = C.c_void_p()
+        check(lib().dh_create(device, C.byref(self._h)))
+        self.device = device
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().dh_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def synchronize(self) -> None:
+        check(lib().dh_synchronize(self._h))
+
+    def memory_info(self) -> tuple[int, int]:
+        f, t = C.c_size_t(), C.c_size_t()
+        check(lib().dh_memory_info(self._h, C.byref(f), C.byref(t)))
+        return f.value, t.value
+
+
+def is_available() -> bool:
+    return bool(lib().dh_is_available())
+
+
+class Pool:
+    """Device page pool [P][2][Hkv][16][D] (+ scale records)."""
+
+    def __init__(self, backend: Backend, num_pages: int, num_kv_heads: int, head_dim: int,
+                 kv_format: int = _lib.KV_BF16, page_size: int = _lib.PAGE_SIZE):
+        self.backend = backend
+        self._h = C.c_void_p()
+        check(lib().dh_pool_create(backend._h, num_pages, num_kv_heads, head_dim, page_size,
+                                   kv_format, C.byref(self._h)))
+        self.num_pages = num_pages
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.kv_format = kv_format
+        self.page_bytes = lib().dh_pool_page_bytes(self._h)
+        self.scale_bytes = lib().dh_pool_scale_bytes(self._h)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().dh_pool_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def write_pages(self, page_ids, data: np.ndarray, scales: Optional[np.ndarray] = None,
+                    stream=None) -> None:
+        ids = np.ascontiguousarray(page_ids, dtype=np.uint32)
+        data = np.ascontiguousarray(data)
+        assert data.nbytes == len(ids) * self.page_bytes, "data size does not match the pages"
+        sp = None
+        if self.scale_bytes:
+            scales = np.ascontiguousarray(scales)
+            assert scales.nbytes == len(ids) * self.scale_bytes, "scale size does not match the pages"
+            sp = scales.ctypes.data_as(C.c_void_p)
+        check(lib().dh_pool_write_pages(self._h, ids.ctypes.data_as(_lib._PU32), len(ids),
+                                        data.ctypes.data_as(C.c_void_p), sp,
+                                        _stream_ptr(stream) if stream is not None else None))
+
+    def write_tokens(self, page_id: int, tok_offset: int, k: np.ndarray, v: np.ndarray,
+                     k_scale=None, v_scale=None, stream=None) -> None:
+        """k, v: [num_kv_heads][n_tok][head_dim] in the pool's element format."""
+        k = np.ascontiguousarray(k)
+        v = np.ascontiguousarray(v)
+        n_tok = k.shape[1]
+        ks = None if k_scale is None else np.ascontiguousarray(k_scale)
+        vs = None if v_scale is None else np.ascontiguousarray(v_scale)
+        check(lib().dh_pool_write_tokens(self._h, page_id, tok_offset, n_tok,
+                                         k.ctypes.data_as(C.c_void_p), v.ctypes.data_as(C.c_void_p),
+                                         None if ks is None else ks.ctypes.data_as(C.c_void_p),
+                                         None if vs is None else vs.ctypes.data_as(C.c_void_p),
+                                         _stream_ptr(stream) if stream is not None else None))
+        if stream is None:
+            self.backend.synchronize()
+
+    def copy_page(self, src: int, dst: int, stream=None) -> None:
+        check(lib().dh_pool_copy_page(self._h, src, dst,
+                                      _stream_ptr(stream) if stream is not None else None))
+
+    def read_page(self, page_id: int) -> tuple[np.ndarray, Optional[np.ndarray]]:
+        data = np.empty(self.page_bytes, dtype=np.uint8)
+        scales = np.empty(self.scale_bytes, dtype=np.uint8) if self.scale_bytes else None
+        check(lib().dh_pool_read_page(self._h, page_id, data.ctypes.data_as(C.c_void_p),
+                                      None if scales is None else scales.ctypes.data_as(C.c_void_p)))
+        return data, scales
+
+    def gather(self, page_ids, kv_head: int):
+        """dh_gather_debug: [2][n][16][D] raw bytes of the selected planes."""
+        torch = _torch()
+        ids = np.ascontiguousarray(page_ids, dtype=np.uint32)
+        eb = self.page_bytes // (2 * self.num_kv_heads * 16 * self.head_dim)
+        out = torch.empty(max(1, 2 * len(ids) * 16 * self.head_dim * eb), dtype=torch.uint8,
+                          device=f"cuda:{self.backend.device}")
+        n_out = C.c_uint32()
+        check(lib().dh_gather_debug(self._h, ids.ctypes.data_as(_lib._PU32), len(ids), kv_head,
+                                    C.c_void_p(out.data_ptr()), C.byref(n_out), None))
+        n = n_out.value
+        return out[: 2 * n * 16 * self.head_dim * eb].cpu().numpy(), n
+
+
+class DecodePlan:
+    """dh_plan: the work decomposition of one decode step."""
+
+    def __init__(self, backend: Backend, config: AttentionConfig, pool: Pool, indptr, indices,
+                 cascade: bool = True, shared_chunk_pages: int = 0, private_chunk_pages: int = 0,
+                 target_items: int = 0):
+        self.backend = backend
+        self.pool = pool
+        self.config = config
+        ip = np.ascontiguousarray(indptr, dtype=np.uint32)
+        ix = np.ascontiguousarray(indices, dtype=np.uint32)
+        self.batch_size = len(ip) - 1
+        opt = _lib.dh_plan_options()
+        opt.shared_chunk_pages = shared_chunk_pages
+        opt.private_chunk_pages = private_chunk_pages
+        opt.target_items = target_items
+        self._c = config.to_c()
+        self._h = C.c_void_p()
+        check(lib().dh_plan_create(backend._h, C.byref(self._c), pool._h,
+                                   ip.ctypes.data_as(_lib._PU32),
+                                   ix.ctypes.data_as(_lib._PU32) if len(ix) else None,
+                                   self.batch_size,
+                                   _lib.PLAN_CASCADE if cascade else _lib.PLAN_FLAT,
+                                   C.byref(opt), C.byref(self._h)))
+        self.workspace_size = lib().dh_plan_workspace_size(self._h)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().dh_plan_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def stats(self) -> dict:
+        s = _lib.dh_plan_stats()
+        check(lib().dh_plan_get_stats(self._h, C.byref(s)))
+        return {k: getattr(s, k) for k, _ in s._fields_}
+
+    def workspace(self):
+        torch = _torch()
+        return torch.empty(max(256, self.workspace_size), dtype=torch.uint8,
+                           device=f"cuda:{self.backend.device}")
+
+
+def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream=None,
+                 stages: int = 3) -> None:
+    """One decode step through dh_decode_stages (stages=3 is dh_decode_batch).
+    q, out: device tensors [B][Hq][D]; last_page_len: device int32 [B] or None."""
+    lpl = None if last_page_len is None else C.c_void_p(last_page_len.data_ptr())
+    check(lib().dh_decode_stages(plan.backend._h, plan.pool._h, plan._h, C.c_void_p(q.data_ptr()),
+                                 lpl, C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()),
+                                 workspace.numel() * workspace.element_size(), stages,
+                                 C.c_void_p(_stream_ptr(stream))))
+
+
+class HipBackend:
+    """AttentionBackend (backend.rs:61-97) on the HIP decode path.
+
+    Like ReferenceBackend it owns a KV store keyed by physical block id: here a
+    device page pool.  append_kv writes tokens into the page of
+    block_table[position / 16] at offset position % 16 (a whole 16-token block
+    at position 16*b is exactly ReferenceBackend::append_kv's store); decode
+    gathers the stored pages of each table, skipping INVALID and never-written
+    blocks as ReferenceBackend skips blocks it has no KV for."""
+
+    def __init__(self, device: int = 0, num_pages: int = 4096, num_kv_heads: int = 8,
+                 head_dim: int = 128, kv_format: int = _lib.KV_BF16, cascade: bool = True):
+        self.backend = Backend(device)
+        self.pool = Pool(self.backend, num_pages, num_kv_heads, head_dim, kv_format)
+        self.cascade = cascade
+        self.page_len: dict[int, int] = {}
+
+    @classmethod
+    def new(cls, **kw) -> "HipBackend":
+        return cls(**kw)
+
+    def _kv_np(self, t) -> np.ndarray:
+        torch = _torch()
+        want = {_lib.KV_F16: torch.float16, _lib.KV_BF16: torch.bfloat16,
+                _lib.KV_F32: torch.float32}.get(self.pool.kv_format)
+        if want is None:
+            raise DhError(_lib.DH_EUNSUPPORTED, "append_kv of FP8 pages needs pre-quantised pages "
+                          "(use Pool.write_tokens)")
+        t = t.detach().to("cpu").to(want).contiguous()
+        if t.dim() == 4:
+            t = t[0]
+        return t.view(torch.int16 if want != torch.float32 else torch.int32).numpy()
+
+    def append_kv(self, key, value, block_table: BlockTable, position: int) -> None:
+        """key/value: [1, num_kv_heads, n, head_dim]; n + position % 16 <= 16."""
+        block = block_table.get(position // _lib.PAGE_SIZE)
+        if block is None or not block.is_valid():
+            return                                   # backend.rs:296-298: no block, no store
+        off = position % _lib.PAGE_SIZE
+        k = self._kv_np(key)
+        v = self._kv_np(value)
+        if k.shape[0] != self.pool.num_kv_heads or k.shape[2] != self.pool.head_dim:
+            raise DhError(_lib.DH_EINVAL, f"key shape {tuple(key.shape)} does not match the pool")
+        self.pool.write_tokens(int(block), off, k, v)
+        self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + k.shape[1])
+
+    def _csr(self, tables: Sequence[BlockTable]):
+        indptr, indices, lpl = [0], [], []
+        for t in tables:
+            kept = [int(b) for b in t.blocks() if b.is_valid() and self.page_len.get(int(b), 0) > 0]
+            for b in kept[:-1]:
+                if self.page_len[b] != _lib.PAGE_SIZE:
+                    raise DhError(_lib.DH_EUNSUPPORTED,
+                                  f"block {b} holds {self.page_len[b]} tokens but is not the last "
+                                  "stored block of its table")
+            indices.extend(kept)
+            indptr.append(len(indices))
+            lpl.append(self.page_len[kept[-1]] if kept else _lib.PAGE_SIZE)
+        return (np.array(indptr, dtype=np.uint32), np.array(indices, dtype=np.uint32),
+                np.array(lpl, dtype=np.int32))
+
+    def decode_batch(self, queries, block_tables: Sequence[BlockTable], config: AttentionConfig):
+        """queries: list of [1, num_heads, 1, head_dim] tensors; returns the
+        list of outputs, same shape and dtype (backend.rs:267-283)."""
+        torch = _torch()
+        if len(queries) != len(block_tables):
+            raise DhError(_lib.DH_EINVAL, "queries and block_tables differ in length")
+        if not queries:
+            return []
+        dev = f"cuda:{self.backend.device}"
+        qdt = queries[0].dtype
+        cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
+        cfg.scale = config.scale
+        cfg.sliding_window = config.sliding_window
+        cfg.gqa_mapping = config.gqa_mapping
+        cfg.q_dtype = dtype_code(qdt)
+        cfg.kv_format = self.pool.kv_format
+        indptr, indices, lpl = self._csr(block_tables)
+        plan = DecodePlan(self.backend, cfg, self.pool, indptr, indices, cascade=self.cascade)
+        q = torch.stack([x.reshape(config.num_heads, config.head_dim) for x in queries]).to(dev).contiguous()
+        out = torch.empty_like(q)
+        lp = torch.from_numpy(lpl).to(dev)
+        ws = plan.workspace()
+        decode_batch(plan, q, out, ws, lp)
+        torch.cuda.synchronize(dev)
+        return [out[i].reshape(1, config.num_heads, 1, config.head_dim) for i in range(len(queries))]
+
+    def decode(self, query, block_table: BlockTable, config: AttentionConfig):
+        """backend.rs:206-265."""
+        return self.decode_batch([query], [block_table], config)[0]
+
+    def prefill(self, query, key, value, block_table: BlockTable, config: AttentionConfig):
+        raise DhError(_lib.DH_EUNSUPPORTED, "prefill is not implemented on the HIP backend")
+
+
+__all__ = ["AttentionConfig", "Backend", "Pool", "DecodePlan", "decode_batch", "HipBackend",
+           "is_available", "dtype_code", "torch_dtype", "raw_to_tensor"]

@@ -1,0 +1,581 @@
+// C-ABI implementation: backend, device page pool, decode plans and the
+// decode launch.  Replaces crates/dendrite-ffi (cuda.rs device handling and
+// the FlashInfer BatchDecodeKernel / CascadeAttention wrappers) and fills the
+// FlashInferBackend slot of crates/dendrite-core/src/attention/flashinfer.rs.
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "dh_device.hpp"
+#include "dh_internal.hpp"
+#include "planner.hpp"
+
+namespace dh {
+
+static thread_local std::string g_last_error;
+
+dh_status fail(dh_status s, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return s;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int launch_e4m3_debug(const uint32_t* codes, const uint8_t* e8m0, uint32_t n4, uint32_t* out,
+                      void* stream);
+int launch_scatter(uint8_t* dst, const uint8_t* src, const uint32_t* ids, uint32_t n,
+                   uint64_t rec_bytes, void* stream);
+
+}  // namespace dh
+
+using dh::fail;
+
+#define DH_HIP(expr)                                                                      \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess) return fail(DH_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+struct dh_backend {
+    int device;
+};
+
+struct dh_pool {
+    dh_backend* be;
+    uint32_t num_pages, hkv, d, fmt, eb;
+    uint64_t page_bytes, scale_bytes;
+    uint8_t* data;
+    uint8_t* scales;
+};
+
+struct dh_plan {
+    dh_backend* be;
+    dh_attn_config cfg;
+    uint32_t batch;
+    uint32_t pool_pages;
+    uint32_t n_items;
+    uint32_t n_slots;
+    uint8_t* dev;
+    dh::Item* items;
+    uint32_t* pages;
+    dh::SeqSlot* seqslots;
+    uint32_t* slot_ptr;
+    dh_plan_stats stats;
+    size_t ws_bytes;
+    size_t ws_lse_off;
+};
+
+extern "C" {
+
+const char* dh_last_error(void) { return dh::g_last_error.c_str(); }
+const char* dh_version(void) { return "dendrite-hip 0.1.0 (gfx950)"; }
+
+/* ------------------------------------------------------------------ config */
+
+dh_status dh_attn_config_init(dh_attn_config* cfg, uint32_t num_heads, uint32_t num_kv_heads,
+                              uint32_t head_dim) {
+    if (!cfg) return fail(DH_EINVAL, "cfg is NULL");
+    memset(cfg, 0, sizeof *cfg);
+    cfg->num_heads = num_heads;
+    cfg->num_kv_heads = num_kv_heads;
+    cfg->head_dim = head_dim;
+    // backend.rs:37: 1.0 / (head_dim as f32).sqrt(), in f32.
+    cfg->scale = 1.0f / sqrtf(float(head_dim));
+    cfg->sliding_window = 0;
+    cfg->gqa_mapping = DH_GQA_TILED;
+    cfg->q_dtype = DH_DTYPE_BF16;
+    cfg->kv_format = DH_KV_BF16;
+    return DH_OK;
+}
+
+uint32_t dh_attn_config_num_queries_per_kv(const dh_attn_config* cfg) {
+    if (!cfg || cfg->num_kv_heads == 0) return 0;
+    return cfg->num_heads / cfg->num_kv_heads;
+}
+
+static dh_status validate_config(const dh_attn_config* cfg) {
+    if (!cfg) return fail(DH_EINVAL, "config is NULL");
+    if (cfg->num_heads == 0 || cfg->num_kv_heads == 0)
+        return fail(DH_EINVAL, "num_heads and num_kv_heads must be positive");
+    // batch_decode.rs:41-45
+    if (cfg->num_heads % cfg->num_kv_heads != 0)
+        return fail(DH_EINVAL, "num_qo_heads must be divisible by num_kv_heads");
+    // batch_decode.rs:33-39, flashinfer/mod.rs:20
+    if (cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256)
+        return fail(DH_EINVAL, "unsupported head_dim: %u, supported: [64, 128, 256]", cfg->head_dim);
+    if (cfg->sliding_window != 0)
+        return fail(DH_EUNSUPPORTED, "sliding_window is not supported (no Dendrite backend reads it)");
+    if (cfg->gqa_mapping > DH_GQA_INTERLEAVED) return fail(DH_EINVAL, "bad gqa_mapping %u", cfg->gqa_mapping);
+    if (cfg->q_dtype > DH_DTYPE_F32) return fail(DH_EINVAL, "bad q_dtype %u", cfg->q_dtype);
+    if (cfg->kv_format > DH_KV_MXFP8) return fail(DH_EINVAL, "bad kv_format %u", cfg->kv_format);
+    if (!(cfg->scale == cfg->scale) || isinf(cfg->scale)) return fail(DH_EINVAL, "scale must be finite");
+    if (!dh::attend_supported(cfg->q_dtype, cfg->kv_format, cfg->head_dim))
+        return fail(DH_EUNSUPPORTED, "q dtype %u with kv format %u is not supported", cfg->q_dtype,
+                    cfg->kv_format);
+    return DH_OK;
+}
+
+/* ----------------------------------------------------------------- backend */
+
+int dh_is_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n > 0;
+}
+
+dh_status dh_device_count(int* count) {
+    if (!count) return fail(DH_EINVAL, "count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) n = 0;
+    else if (e != hipSuccess) return fail(DH_EHIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
+    *count = n;
+    return DH_OK;
+}
+
+dh_status dh_create(int device, dh_backend** out) {
+    if (!out) return fail(DH_EINVAL, "out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(DH_EUNSUPPORTED, "no HIP device available");
+    if (device < 0 || device >= n) return fail(DH_EINVAL, "device %d out of range (%d devices)", device, n);
+    DH_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    DH_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(DH_EUNSUPPORTED, "device %d is %s; this library is built for gfx950", device,
+                    prop.gcnArchName);
+    dh_backend* be = new (std::nothrow) dh_backend;
+    if (!be) return fail(DH_ENOMEM, "out of host memory");
+    be->device = device;
+    *out = be;
+    return DH_OK;
+}
+
+dh_status dh_destroy(dh_backend* be) {
+    delete be;
+    return DH_OK;
+}
+
+dh_status dh_memory_info(dh_backend* be, size_t* free_b, size_t* total_b) {
+    if (!be || !free_b || !total_b) return fail(DH_EINVAL, "NULL argument");
+    DH_HIP(hipSetDevice(be->device));
+    DH_HIP(hipMemGetInfo(free_b, total_b));
+    return DH_OK;
+}
+
+dh_status dh_synchronize(dh_backend* be) {
+    if (!be) return fail(DH_EINVAL, "backend is NULL");
+    DH_HIP(hipSetDevice(be->device));
+    DH_HIP(hipDeviceSynchronize());
+    return DH_OK;
+}
+
+/* -------------------------------------------------------------------- pool */
+
+dh_status dh_pool_create(dh_backend* be, uint32_t num_pages, uint32_t hkv, uint32_t d,
+                         uint32_t page_size, uint32_t fmt, dh_pool** out) {
+    if (!be || !out) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    if (page_size != DH_PAGE_SIZE) return fail(DH_EINVAL, "page_size must be %u", DH_PAGE_SIZE);
+    if (num_pages == 0 || hkv == 0) return fail(DH_EINVAL, "num_pages and num_kv_heads must be positive");
+    if (d != 64 && d != 128 && d != 256) return fail(DH_EINVAL, "unsupported head_dim: %u", d);
+    const uint32_t eb = dh::kv_elem_bytes(fmt);
+    if (eb == 0) return fail(DH_EINVAL, "bad kv_format %u", fmt);
+    DH_HIP(hipSetDevice(be->device));
+    dh_pool* p = new (std::nothrow) dh_pool;
+    if (!p) return fail(DH_ENOMEM, "out of host memory");
+    p->be = be;
+    p->num_pages = num_pages;
+    p->hkv = hkv;
+    p->d = d;
+    p->fmt = fmt;
+    p->eb = eb;
+    p->page_bytes = uint64_t(2) * hkv * DH_PAGE_SIZE * d * eb;
+    p->scale_bytes = dh::kv_scale_bytes(fmt, hkv, d);
+    p->data = nullptr;
+    p->scales = nullptr;
+    hipError_t e = hipMalloc(&p->data, p->page_bytes * num_pages);
+    if (e != hipSuccess) {
+        delete p;
+        return fail(DH_ENOMEM, "pool allocation of %llu bytes failed: %s",
+                    (unsigned long long)(p->page_bytes * num_pages), hipGetErrorString(e));
+    }
+    e = hipMemset(p->data, 0, p->page_bytes * num_pages);
+    if (e == hipSuccess && p->scale_bytes) {
+        e = hipMalloc(&p->scales, p->scale_bytes * num_pages);
+        if (e == hipSuccess) e = hipMemset(p->scales, 0, p->scale_bytes * num_pages);
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(p->data);
+        if (p->scales) (void)hipFree(p->scales);
+        delete p;
+        return fail(DH_ENOMEM, "pool initialisation failed: %s", hipGetErrorString(e));
+    }
+    *out = p;
+    return DH_OK;
+}
+
+dh_status dh_pool_destroy(dh_pool* p) {
+    if (!p) return DH_OK;
+    (void)hipSetDevice(p->be->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(p->data);
+    if (p->scales) (void)hipFree(p->scales);
+    delete p;
+    return DH_OK;
+}
+
+size_t dh_pool_page_bytes(const dh_pool* p) { return p ? size_t(p->page_bytes) : 0; }
+size_t dh_pool_scale_bytes(const dh_pool* p) { return p ? size_t(p->scale_bytes) : 0; }
+uint32_t dh_pool_num_pages(const dh_pool* p) { return p ? p->num_pages : 0; }
+void* dh_pool_data(dh_pool* p) { return p ? p->data : nullptr; }
+void* dh_pool_scales(dh_pool* p) { return p ? p->scales : nullptr; }
+
+dh_status dh_pool_write_tokens(dh_pool* p, uint32_t page_id, uint32_t tok_offset, uint32_t n_tok,
+                               const void* k, const void* v, const void* k_scale,
+                               const void* v_scale, void* stream) {
+    if (!p || !k || !v) return fail(DH_EINVAL, "NULL argument");
+    if (page_id >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", page_id);
+    if (n_tok == 0 || tok_offset + n_tok > DH_PAGE_SIZE)
+        return fail(DH_EINVAL, "tokens [%u, %u) do not fit a %u-token page", tok_offset,
+                    tok_offset + n_tok, DH_PAGE_SIZE);
+    if ((p->fmt == DH_KV_FP8_E4M3 || p->fmt == DH_KV_MXFP8) && (!k_scale || !v_scale))
+        return fail(DH_EINVAL, "scales are required for this kv format");
+    DH_HIP(hipSetDevice(p->be->device));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const uint64_t row = uint64_t(p->d) * p->eb;
+    for (uint32_t plane = 0; plane < 2; ++plane) {
+        const uint8_t* src = static_cast<const uint8_t*>(plane ? v : k);
+        for (uint32_t h = 0; h < p->hkv; ++h) {
+            uint8_t* dst = p->data + dh::plane_offset(page_id, plane, h, p->hkv, p->d, p->eb) +
+                           uint64_t(tok_offset) * row;
+            DH_HIP(hipMemcpyAsync(dst, src + uint64_t(h) * n_tok * row, n_tok * row,
+                                  hipMemcpyHostToDevice, s));
+        }
+    }
+    if (p->fmt == DH_KV_FP8_E4M3) {
+        for (uint32_t plane = 0; plane < 2; ++plane) {
+            uint8_t* dst = p->scales + (uint64_t(page_id) * 2 + plane) * p->hkv * 4;
+            DH_HIP(hipMemcpyAsync(dst, plane ? v_scale : k_scale, p->hkv * 4, hipMemcpyHostToDevice, s));
+        }
+    } else if (p->fmt == DH_KV_MXFP8) {
+        const uint64_t G = p->d / 32;
+        for (uint32_t plane = 0; plane < 2; ++plane) {
+            const uint8_t* src = static_cast<const uint8_t*>(plane ? v_scale : k_scale);
+            for (uint32_t h = 0; h < p->hkv; ++h) {
+                uint8_t* dst = p->scales + ((uint64_t(page_id) * 2 + plane) * p->hkv + h) * DH_PAGE_SIZE * G +
+                               uint64_t(tok_offset) * G;
+                DH_HIP(hipMemcpyAsync(dst, src + uint64_t(h) * n_tok * G, n_tok * G,
+                                      hipMemcpyHostToDevice, s));
+            }
+        }
+    }
+    return DH_OK;
+}
+
+dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const void* data,
+                              const void* scales, void* stream) {
+    if (!p || (n && (!ids || !data))) return fail(DH_EINVAL, "NULL argument");
+    if (p->scale_bytes && n && !scales) return fail(DH_EINVAL, "scales are required for this kv format");
+    for (uint32_t i = 0; i < n; ++i)
+        if (ids[i] >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", ids[i]);
+    if (n == 0) return DH_OK;
+    DH_HIP(hipSetDevice(p->be->device));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const uint32_t batch = std::min<uint32_t>(n, std::max<uint64_t>(1, (256ull << 20) / p->page_bytes));
+    uint8_t* stage = nullptr;
+    uint32_t* dids = nullptr;
+    DH_HIP(hipMalloc(&stage, batch * (p->page_bytes + p->scale_bytes)));
+    hipError_t e = hipMalloc(&dids, batch * sizeof(uint32_t));
+    dh_status st = DH_OK;
+    for (uint32_t i0 = 0; e == hipSuccess && i0 < n; i0 += batch) {
+        const uint32_t m = std::min(batch, n - i0);
+        e = hipMemcpyAsync(dids, ids + i0, m * sizeof(uint32_t), hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(stage, static_cast<const uint8_t*>(data) + uint64_t(i0) * p->page_bytes,
+                               uint64_t(m) * p->page_bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipError_t(dh::launch_scatter(p->data, stage, dids, m, p->page_bytes, s));
+        if (e == hipSuccess && p->scale_bytes) {
+            uint8_t* sst = stage + uint64_t(batch) * p->page_bytes;
+            e = hipMemcpyAsync(sst, static_cast<const uint8_t*>(scales) + uint64_t(i0) * p->scale_bytes,
+                               uint64_t(m) * p->scale_bytes, hipMemcpyHostToDevice, s);
+            if (e == hipSuccess) e = hipError_t(dh::launch_scatter(p->scales, sst, dids, m, p->scale_bytes, s));
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    if (e != hipSuccess) st = fail(DH_EHIP, "page upload failed: %s", hipGetErrorString(e));
+    (void)hipFree(stage);
+    if (dids) (void)hipFree(dids);
+    return st;
+}
+
+dh_status dh_pool_copy_page(dh_pool* p, uint32_t src, uint32_t dst, void* stream) {
+    if (!p) return fail(DH_EINVAL, "pool is NULL");
+    if (src >= p->num_pages || dst >= p->num_pages)
+        return fail(DH_EINVAL, "page id outside the pool (src %u, dst %u)", src, dst);
+    if (src == dst) return DH_OK;
+    DH_HIP(hipSetDevice(p->be->device));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    DH_HIP(hipMemcpyAsync(p->data + uint64_t(dst) * p->page_bytes, p->data + uint64_t(src) * p->page_bytes,
+                          p->page_bytes, hipMemcpyDeviceToDevice, s));
+    if (p->scale_bytes)
+        DH_HIP(hipMemcpyAsync(p->scales + uint64_t(dst) * p->scale_bytes,
+                              p->scales + uint64_t(src) * p->scale_bytes, p->scale_bytes,
+                              hipMemcpyDeviceToDevice, s));
+    return DH_OK;
+}
+
+dh_status dh_pool_read_page(dh_pool* p, uint32_t page_id, void* data_out, void* scales_out) {
+    if (!p || !data_out) return fail(DH_EINVAL, "NULL argument");
+    if (page_id >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", page_id);
+    DH_HIP(hipSetDevice(p->be->device));
+    DH_HIP(hipDeviceSynchronize());
+    DH_HIP(hipMemcpy(data_out, p->data + uint64_t(page_id) * p->page_bytes, p->page_bytes,
+                     hipMemcpyDeviceToHost));
+    if (p->scale_bytes && scales_out)
+        DH_HIP(hipMemcpy(scales_out, p->scales + uint64_t(page_id) * p->scale_bytes, p->scale_bytes,
+                         hipMemcpyDeviceToHost));
+    return DH_OK;
+}
+
+/* -------------------------------------------------------------------- plan */
+
+static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                         const uint32_t* indptr, const uint32_t* indices, uint32_t batch,
+                         uint32_t flags, const dh_plan_options* opt, dh_plan** out) {
+    if (!be || !pool || !out) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    dh_status st = validate_config(cfg);
+    if (st != DH_OK) return st;
+    if (pool->hkv != cfg->num_kv_heads || pool->d != cfg->head_dim || pool->fmt != cfg->kv_format)
+        return fail(DH_EINVAL, "pool (kv heads %u, head_dim %u, format %u) does not match the config "
+                    "(%u, %u, %u)", pool->hkv, pool->d, pool->fmt, cfg->num_kv_heads, cfg->head_dim,
+                    cfg->kv_format);
+    if (batch && !indptr) return fail(DH_EINVAL, "indptr is NULL");
+    if (batch && indptr[batch] > indptr[0] && !indices) return fail(DH_EINVAL, "indices is NULL");
+    if (flags & ~DH_PLAN_CASCADE) return fail(DH_EINVAL, "unknown plan flags 0x%x", flags);
+
+    dh::PlanInput in;
+    in.batch = batch;
+    std::vector<uint32_t> zero_ptr(1, 0);
+    in.indptr = batch ? indptr : zero_ptr.data();
+    in.indices = indices;
+    in.num_pool_pages = pool->num_pages;
+    in.hq = cfg->num_heads;
+    in.hkv = cfg->num_kv_heads;
+    in.rows_per_item = cfg->q_dtype == DH_DTYPE_F32 ? 16 : dh::kRowsPerItem;
+    in.cascade = (flags & DH_PLAN_CASCADE) != 0;
+    if (opt) {
+        in.shared_chunk_pages = opt->shared_chunk_pages;
+        in.private_chunk_pages = opt->private_chunk_pages;
+        in.target_items = opt->target_items;
+    }
+    dh::HostPlan hp;
+    std::string err;
+    int rc = dh::build_plan(in, hp, err);
+    if (rc != DH_OK) return fail(dh_status(rc), "%s", err.c_str());
+
+    dh_plan* pl = new (std::nothrow) dh_plan;
+    if (!pl) return fail(DH_ENOMEM, "out of host memory");
+    memset(pl, 0, sizeof *pl);
+    pl->be = be;
+    pl->cfg = *cfg;
+    pl->batch = batch;
+    pl->pool_pages = pool->num_pages;
+    pl->n_items = uint32_t(hp.items.size());
+    pl->n_slots = hp.num_slots;
+    const size_t o_items = 0;
+    const size_t o_pages = align_up(o_items + hp.items.size() * sizeof(dh::Item), 256);
+    const size_t o_ss = align_up(o_pages + hp.pages.size() * sizeof(uint32_t), 256);
+    const size_t o_sp = align_up(o_ss + hp.seqslots.size() * sizeof(dh::SeqSlot), 256);
+    const size_t total = align_up(o_sp + hp.slot_ptr.size() * sizeof(uint32_t), 256);
+    std::vector<uint8_t> blob(total, 0);
+    memcpy(blob.data() + o_items, hp.items.data(), hp.items.size() * sizeof(dh::Item));
+    memcpy(blob.data() + o_pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
+    memcpy(blob.data() + o_ss, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
+    memcpy(blob.data() + o_sp, hp.slot_ptr.data(), hp.slot_ptr.size() * sizeof(uint32_t));
+    hipError_t e = hipSetDevice(be->device);
+    if (e == hipSuccess) e = hipMalloc(&pl->dev, total);
+    if (e == hipSuccess) e = hipMemcpy(pl->dev, blob.data(), total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (pl->dev) (void)hipFree(pl->dev);
+        delete pl;
+        return fail(DH_EHIP, "plan upload failed: %s", hipGetErrorString(e));
+    }
+    pl->items = reinterpret_cast<dh::Item*>(pl->dev + o_items);
+    pl->pages = reinterpret_cast<uint32_t*>(pl->dev + o_pages);
+    pl->seqslots = reinterpret_cast<dh::SeqSlot*>(pl->dev + o_ss);
+    pl->slot_ptr = reinterpret_cast<uint32_t*>(pl->dev + o_sp);
+    const size_t rows = size_t(hp.num_slots) * cfg->num_heads;
+    pl->ws_lse_off = align_up(rows * cfg->head_dim * sizeof(float), 256);
+    pl->ws_bytes = align_up(pl->ws_lse_off + rows * sizeof(float), 256);
+    pl->stats.batch_size = batch;
+    pl->stats.num_segments = hp.num_segments;
+    pl->stats.num_shared_segments = hp.num_shared_segments;
+    pl->stats.num_items = pl->n_items;
+    pl->stats.num_partials = hp.num_slots;
+    pl->stats.unique_pages = hp.unique_pages;
+    pl->stats.page_reads = hp.page_reads;
+    pl->stats.total_pages = hp.total_pages;
+    *out = pl;
+    return DH_OK;
+}
+
+dh_status dh_plan_destroy(dh_plan* pl) {
+    if (!pl) return DH_OK;
+    (void)hipSetDevice(pl->be->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(pl->dev);
+    delete pl;
+    return DH_OK;
+}
+
+size_t dh_plan_workspace_size(const dh_plan* pl) { return pl ? pl->ws_bytes : 0; }
+
+dh_status dh_plan_get_stats(const dh_plan* pl, dh_plan_stats* st) {
+    if (!pl || !st) return fail(DH_EINVAL, "NULL argument");
+    *st = pl->stats;
+    return DH_OK;
+}
+
+/* ------------------------------------------------------------------ decode */
+
+dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
+                           uint32_t mask, void* stream) {
+    if (!be || !pool || !pl) return fail(DH_EINVAL, "NULL argument");
+    if (pl->be != be || pool->be != be) return fail(DH_EINVAL, "plan/pool belong to another backend");
+    if (pool->num_pages != pl->pool_pages || pool->hkv != pl->cfg.num_kv_heads ||
+        pool->d != pl->cfg.head_dim || pool->fmt != pl->cfg.kv_format)
+        return fail(DH_EINVAL, "pool does not match the plan");
+    if (pl->batch == 0) return DH_OK;
+    if (!q || !out) return fail(DH_EINVAL, "q and out must be device pointers");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(DH_EINVAL, "q and out must be 16-byte aligned");
+    if (ws_bytes < pl->ws_bytes || (pl->ws_bytes && !ws))
+        return fail(DH_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes the plan needs",
+                    ws_bytes, pl->ws_bytes);
+    if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
+    DH_HIP(hipSetDevice(be->device));
+    const dh_attn_config& c = pl->cfg;
+    float* ws_o = static_cast<float*>(ws);
+    float* ws_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
+    if (mask & 1u) {
+        dh::AttendArgs a;
+        a.items = pl->items;
+        a.pages = pl->pages;
+        a.seqslots = pl->seqslots;
+        a.q = q;
+        a.kv = pool->data;
+        a.scales = pool->scales;
+        a.last_page_len = last_page_len;
+        a.ws_o = ws_o;
+        a.ws_lse = ws_lse;
+        a.hq = c.num_heads;
+        a.hkv = c.num_kv_heads;
+        a.r = c.num_heads / c.num_kv_heads;
+        a.gqa_tiled = c.gqa_mapping == DH_GQA_TILED ? 1u : 0u;
+        a.scale_log2 = c.scale * 1.4426950408889634f;
+        hipError_t e = hipError_t(dh::launch_attend(a, pl->n_items, c.q_dtype, c.kv_format, c.head_dim, stream));
+        if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+    }
+    if (mask & 2u) {
+        dh::MergeArgs m;
+        m.slot_ptr = pl->slot_ptr;
+        m.ws_o = ws_o;
+        m.ws_lse = ws_lse;
+        m.out = out;
+        m.batch = pl->batch;
+        m.hq = c.num_heads;
+        hipError_t e = hipError_t(dh::launch_merge(m, c.q_dtype, c.head_dim, stream));
+        if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
+    }
+    return DH_OK;
+}
+
+dh_status dh_decode_batch(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                          const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
+                          void* stream) {
+    return dh_decode_stages(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream);
+}
+
+/* ------------------------------------------------------------------- merge */
+
+dh_status dh_merge_states(const float* o_a, const float* lse_a, const float* o_b, const float* lse_b,
+                          float* o_out, float* lse_out, uint32_t n_rows, uint32_t d, void* stream) {
+    if (n_rows == 0) return DH_OK;
+    if (!o_a || !lse_a || !o_b || !lse_b || !o_out || !lse_out) return fail(DH_EINVAL, "NULL argument");
+    if (d == 0 || d > 1024) return fail(DH_EINVAL, "head_dim %u out of range", d);
+    hipError_t e = hipError_t(dh::launch_merge_states(o_a, lse_a, o_b, lse_b, o_out, lse_out, n_rows, d, stream));
+    if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+
+/* ------------------------------------------------------------------ gather */
+
+dh_status dh_gather_debug(const dh_pool* pool, const uint32_t* ids, uint32_t n, uint32_t kv_head,
+                          void* out, uint32_t* n_out, void* stream) {
+    if (!pool || !out || !n_out || (n && !ids)) return fail(DH_EINVAL, "NULL argument");
+    if (kv_head >= pool->hkv) return fail(DH_EINVAL, "kv head %u out of range", kv_head);
+    std::vector<uint32_t> sel;
+    sel.reserve(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (ids[i] == DH_INVALID_PAGE) continue;
+        if (ids[i] >= pool->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", ids[i]);
+        sel.push_back(ids[i]);
+    }
+    *n_out = uint32_t(sel.size());
+    if (sel.empty()) return DH_OK;
+    DH_HIP(hipSetDevice(pool->be->device));
+    uint32_t* d_ids = nullptr;
+    DH_HIP(hipMalloc(&d_ids, sel.size() * sizeof(uint32_t)));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(d_ids, sel.data(), sel.size() * sizeof(uint32_t), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipError_t(dh::launch_gather(pool->data, d_ids, uint32_t(sel.size()), kv_head, pool->hkv, pool->d,
+                                         pool->eb, static_cast<uint8_t*>(out), s));
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(d_ids);
+    if (e != hipSuccess) return fail(DH_EHIP, "gather failed: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+
+dh_status dh_debug_e4m3_to_bf16(int device, const uint8_t* codes, const uint8_t* e8m0, uint32_t n,
+                                uint16_t* out) {
+    if (n % 4) return fail(DH_EINVAL, "n must be a multiple of 4");
+    if (n == 0) return DH_OK;
+    if (!codes || !e8m0 || !out) return fail(DH_EINVAL, "NULL argument");
+    DH_HIP(hipSetDevice(device));
+    uint8_t* buf = nullptr;
+    const size_t nb = size_t(n) + n / 4 + size_t(n) * 2;
+    DH_HIP(hipMalloc(&buf, nb));
+    hipError_t e = hipMemcpy(buf, codes, n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(buf + n, e8m0, n / 4, hipMemcpyHostToDevice);
+    uint32_t* dout = reinterpret_cast<uint32_t*>(buf + ((size_t(n) + n / 4 + 3) / 4) * 4);
+    if (e == hipSuccess)
+        e = hipError_t(dh::launch_e4m3_debug(reinterpret_cast<const uint32_t*>(buf), buf + n, n / 4, dout, nullptr));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(out, dout, size_t(n) * 2, hipMemcpyDeviceToHost);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return fail(DH_EHIP, "debug conversion failed: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+
+}  // extern "C"

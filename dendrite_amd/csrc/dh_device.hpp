@@ -1,0 +1,93 @@
+// Structures shared by the host planner/launcher and the gfx950 kernels.
+//
+// A decode step is cut into work items.  One item is attended by one
+// workgroup of four wave64s: a run of pages (all 16-token pages of one chunk
+// of a segment), one KV head and up to 32 query rows.  A segment is either a
+// run of pages shared by several sequences (a tree-shared prefix, the CoW
+// sharing TreeState::fork creates, crates/dendrite-core/src/tree/state.rs:
+// 49-84) or one sequence's private tail.  Every item writes one partial
+// attention state (O normalised, log2-sum-exp) per query row into the
+// workspace; the merge kernel combines the partial states of each
+// (sequence, query head) by log-sum-exp into the output.
+#pragma once
+#include <stdint.h>
+#include <stddef.h>
+
+#if defined(__HIPCC__)
+#define DH_HOST_DEVICE __host__ __device__
+#else
+#define DH_HOST_DEVICE
+#endif
+
+namespace dh {
+
+constexpr int kPageSize = 16;       // tokens per page (dendrite-ffi flashinfer/mod.rs:14)
+constexpr int kWaves = 4;           // wave64s per attention workgroup
+constexpr int kRowsPerItem = 32;    // query rows per item (two 16-row MFMA tiles)
+
+// One attention work item (32 bytes, read once per workgroup).
+struct Item {
+    uint32_t page_off;   // first page of the item in Plan::pages
+    uint32_t npages;     // pages in the item (>= 1)
+    uint32_t seq_off;    // first SeqSlot of the item's (segment, chunk)
+    uint32_t row_begin;  // first row; row rho -> seq_local = rho / r, j = rho % r
+    uint32_t nrows;      // rows in the item, 1..kRowsPerItem
+    uint32_t kv_head;
+    uint32_t flags;      // kItemTail: the item's last page is tail_seq's last page
+    uint32_t tail_seq;
+};
+constexpr uint32_t kItemTail = 1u;
+
+// Sequence of a (segment, chunk) and the partial-state slot it owns there.
+struct SeqSlot {
+    uint32_t seq;
+    uint32_t slot;
+};
+
+struct AttendArgs {
+    const Item* items;
+    const uint32_t* pages;
+    const SeqSlot* seqslots;
+    const void* q;               // [B][Hq][D]
+    const uint8_t* kv;           // pool data [P][2][Hkv][16][D]
+    const void* scales;          // pool scale records (format dependent)
+    const int32_t* last_page_len;
+    float* ws_o;                 // [slots][Hq][D] normalised partial O
+    float* ws_lse;               // [slots][Hq] log2-sum-exp of scaled scores
+    uint32_t hq, hkv, r, gqa_tiled;
+    float scale_log2;            // softmax scale * log2(e)
+};
+
+struct MergeArgs {
+    const uint32_t* slot_ptr;    // [B+1] partial slots of sequence b
+    const float* ws_o;
+    const float* ws_lse;
+    void* out;                   // [B][Hq][D]
+    uint32_t batch, hq;
+};
+
+// Byte offset of the (page, plane, kv head) 16 x D block in the pool.
+DH_HOST_DEVICE inline uint64_t plane_offset(uint32_t page, uint32_t plane, uint32_t head,
+                                                 uint32_t hkv, uint32_t head_dim,
+                                                 uint32_t elem_bytes) {
+    return ((uint64_t(page) * 2u + plane) * hkv + head) * uint64_t(kPageSize) * head_dim *
+           elem_bytes;
+}
+
+}  // namespace dh
+
+// Kernel launchers (defined in decode_kernels.hip).  Return hipError_t as int.
+extern "C++" {
+namespace dh {
+int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint32_t kv_format,
+                  uint32_t head_dim, void* stream);
+int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t head_dim, void* stream);
+int launch_merge_states(const float* o_a, const float* lse_a, const float* o_b,
+                        const float* lse_b, float* o_out, float* lse_out, uint32_t n_rows,
+                        uint32_t head_dim, void* stream);
+int launch_gather(const uint8_t* kv, const uint32_t* pages, uint32_t n_pages, uint32_t kv_head,
+                  uint32_t hkv, uint32_t head_dim, uint32_t elem_bytes, uint8_t* out,
+                  void* stream);
+bool attend_supported(uint32_t q_dtype, uint32_t kv_format, uint32_t head_dim);
+}  // namespace dh
+}

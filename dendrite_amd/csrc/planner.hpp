@@ -1,0 +1,39 @@
+// Host-side decomposition of one decode step into attention work items.
+#pragma once
+#include <stdint.h>
+#include <string>
+#include <vector>
+#include "dh_device.hpp"
+
+namespace dh {
+
+struct PlanInput {
+    uint32_t batch = 0;
+    const uint32_t* indptr = nullptr;   // [batch + 1]
+    const uint32_t* indices = nullptr;  // [indptr[batch]]
+    uint32_t num_pool_pages = 0;
+    uint32_t hq = 0, hkv = 0;
+    uint32_t rows_per_item = kRowsPerItem;
+    bool cascade = true;
+    uint32_t shared_chunk_pages = 0;    // 0 = default
+    uint32_t private_chunk_pages = 0;
+    uint32_t target_items = 0;
+};
+
+struct HostPlan {
+    std::vector<Item> items;
+    std::vector<uint32_t> pages;
+    std::vector<SeqSlot> seqslots;
+    std::vector<uint32_t> slot_ptr;     // [batch + 1]
+    uint32_t num_slots = 0;
+    uint32_t num_segments = 0;
+    uint32_t num_shared_segments = 0;
+    uint64_t unique_pages = 0;
+    uint64_t page_reads = 0;            // pages read per KV head per step
+    uint64_t total_pages = 0;
+};
+
+// Returns 0 on success, else a dh_status code with `err` set.
+int build_plan(const PlanInput& in, HostPlan& out, std::string& err);
+
+}  // namespace dh

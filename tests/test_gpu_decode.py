@@ -1,0 +1,74 @@
+"""GPU parity of the decode path against the CPU oracle (identical seeded
+inputs) for the five benchmark configurations and reduced variants.
+
+Tolerances (from the benchmark contract): f32 1e-4 max-abs; bf16 / FP8 /
+MXFP8 2e-2 max-abs after dequantisation with the same scales, measured beyond
+the output dtype's own rounding (half an ulp of the exact value; see
+tests/_helpers.excess_err).
+"""
+import numpy as np
+import pytest
+
+from dendrite_amd import _lib, workloads
+from tests._helpers import TOL, GpuRun, excess_err, max_abs_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(w, backend, cascade=True, seqs=None, **kw):
+    print(f"[case] {w.name} cascade={cascade} batch={w.batch} kw={kw}", flush=True)
+    run = GpuRun(w, backend, cascade=cascade, **kw)
+    got = run.run()
+    if seqs is not None:
+        got = got[np.asarray(seqs)]
+    ref = run.reference(seqs=seqs)
+    raw = max_abs_err(got, ref)
+    err = excess_err(got, ref, w.q_dtype)
+    print(f"[case] {w.name}: max abs err {raw:.3e}, beyond output rounding {err:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    assert err <= TOL[w.q_dtype], f"{w.name}: error beyond output rounding {err} > {TOL[w.q_dtype]}"
+    return run, err
+
+
+def test_c1_f32(backend):
+    _check(workloads.c1(), backend)
+
+
+@pytest.mark.parametrize("cascade", [True, False])
+def test_c2_bf16_fork(backend, cascade):
+    _check(workloads.c2(), backend, cascade=cascade)
+
+
+@pytest.mark.parametrize("cascade", [True, False])
+def test_c3_small_tree(backend, cascade):
+    w = workloads.c3(root_pages=40, levels=2, level_pages=3, pool_pages=4096)
+    _check(w, backend, cascade=cascade)
+
+
+def test_c3_full_tree_sampled(backend):
+    w = workloads.c3()
+    run, _ = _check(w, backend, seqs=[0, 5, 21, 42, 63])
+    st = run.plan.stats()
+    # Every page of the tree is read once per KV head per step.
+    assert st["page_reads"] == st["unique_pages"] == 1184
+
+
+def test_c4_small_fp8(backend):
+    w = workloads.c4(n_seqs=24, tmin=40, tmax=700, pool_pages=4096)
+    _check(w, backend)
+
+
+def test_c4_full_fp8_sampled(backend):
+    w = workloads.c4()
+    _check(w, backend, seqs=[0, 7, 15, 100, 255])
+
+
+def test_c5_small_mxfp8(backend):
+    w = workloads.c5(requests=2, prefix_pages=40, beams=4, suffix_pages=5, pool_pages=2048)
+    _check(w, backend)
+
+
+def test_interleaved_gqa(backend):
+    w = workloads.c2(branches=3, prefix_pages=12, suffix_pages=3, pool_pages=128)
+    w.gqa_mapping = _lib.GQA_INTERLEAVED
+    _check(w, backend)
