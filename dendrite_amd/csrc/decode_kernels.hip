@@ -123,12 +123,16 @@ __device__ __forceinline__ int item_last_len(const AttendArgs& a, const Item& it
     return (L <= 0 || L > kPageSize) ? kPageSize : L;
 }
 
-// Shared combine stage: waves hold per-row (m, l_partial, O) for `RT` tiles of
-// 16 rows; O[rt][e][i] is element d = (4g+i)*EPL + e of row 16*rt + c.
+// Cross-wave combine.  Each wave holds, per row of its RT tiles of 16 rows,
+// (m, l_partial, O) with O[rt][e][i] = element d = (4g+i)*EPL + e of row
+// 16*rt + c.  The waves rescale their O to the workgroup's row maximum and
+// store it to their own LDS region; the sum over regions, divided by the
+// summed l, is the item's partial state.  (Plain stores: LDS float atomics
+// are far slower here.)
 template <int D, int RT, int EPL>
 struct Combine {
     static constexpr int kStride = D + 4;
-    float o[RT * 16 * kStride];
+    float o[kWaves][RT * 16 * kStride];
     float m[kWaves][RT * 16];
     float l[kWaves][RT * 16];
     float inv[RT * 16];
@@ -142,12 +146,11 @@ __device__ __forceinline__ void combine_and_store(const AttendArgs& a, const Ite
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        if (rt >= nrt) break;
         float lt = l[rt] + __shfl_xor(l[rt], 16);
         lt += __shfl_xor(lt, 32);
         if (g == 0) {
-            sm.m[wave][rt * 16 + c] = m[rt];
-            sm.l[wave][rt * 16 + c] = lt;
+            sm.m[wave][rt * 16 + c] = rt < nrt ? m[rt] : kNegInf;
+            sm.l[wave][rt * 16 + c] = rt < nrt ? lt : 0.f;
         }
     }
     __syncthreads();
@@ -158,17 +161,19 @@ __device__ __forceinline__ void combine_and_store(const AttendArgs& a, const Ite
         float M = sm.m[0][row];
         #pragma unroll
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm.m[w][row]);
-        const float w8 = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - M);
-        if (w8 != 0.f) {
-            float* orow = sm.o + row * Smem::kStride;
+        if (m[rt] == kNegInf) continue;        // this wave saw no token: region unused
+        const float w8 = fast_exp2(m[rt] - M);
+        float* orow = sm.o[wave] + row * Smem::kStride;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
             #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                #pragma unroll
-                for (int i = 0; i < 4; ++i) atomicAdd(orow + (4 * g + i) * EPL + e, O[rt][e][i] * w8);
+            for (int e = 0; e < EPL; e += 4) {
+                f4 v = {O[rt][e][i] * w8, O[rt][e + 1][i] * w8, O[rt][e + 2][i] * w8,
+                        O[rt][e + 3][i] * w8};
+                *reinterpret_cast<f4*>(orow + (4 * g + i) * EPL + e) = v;
             }
         }
     }
-    __syncthreads();
     const int nrows = (int)it.nrows;
     if (tid < nrows) {
         float M = sm.m[0][tid];
@@ -176,7 +181,7 @@ __device__ __forceinline__ void combine_and_store(const AttendArgs& a, const Ite
         float lt = 0.f;
         if (M != kNegInf) {
             for (int w = 0; w < kWaves; ++w) {
-                float mw = sm.m[w][tid];
+                const float mw = sm.m[w][tid];
                 if (mw != kNegInf) lt += sm.l[w][tid] * fast_exp2(mw - M);
             }
         }
@@ -191,32 +196,286 @@ __device__ __forceinline__ void combine_and_store(const AttendArgs& a, const Ite
     constexpr int Q4 = D / 4;
     for (int idx = tid; idx < nrows * Q4; idx += kWaves * 64) {
         const int row = idx / Q4, dq = idx - row * Q4;
-        const float s = sm.inv[row];
-        const float* src = sm.o + row * Smem::kStride + 4 * dq;
-        f4 v = {src[0] * s, src[1] * s, src[2] * s, src[3] * s};
-        *reinterpret_cast<f4*>(a.ws_o + uint64_t(sm.dst[row]) * D + 4 * dq) = v;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            if (sm.m[w][row] == kNegInf) continue;
+            acc += *reinterpret_cast<const f4*>(sm.o[w] + row * Smem::kStride + 4 * dq);
+        }
+        *reinterpret_cast<f4*>(a.ws_o + uint64_t(sm.dst[row]) * D + 4 * dq) = acc * sm.inv[row];
     }
 }
 
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
+//
+// Each wave walks its pairs of pages with the loads of the next pair in
+// flight behind the current pair's math: K of pair i+1 is requested as soon
+// as the score MFMAs of pair i have consumed K, V of pair i+1 as soon as the
+// PV MFMAs have consumed V, so no extra registers hold a second buffer.
+
+// Raw pool bytes of one page for this lane (K rows of token c, V rows of
+// tokens 4g..4g+3), plus the MX scale bytes that go with them.
+template <int D, uint32_t KVF>
+struct PageRaw {
+    static constexpr bool FP8 = (KVF == KVF_FP8 || KVF == KVF_MX);
+    static constexpr int KB = D / 32;
+    static constexpr int EPL = D / 16;
+    static constexpr int KW = FP8 ? 2 : 4;           // dwords per k-chunk
+    static constexpr int VW = FP8 ? EPL / 4 : EPL / 2;
+    static constexpr int G = D / 32;                 // MX groups per token
+    uint32_t k[KB][KW];
+    uint32_t v[4][VW];
+    uint32_t ksc[KVF == KVF_MX ? G : 1];            // MX: K scale byte per k-chunk
+    uint32_t vsc[KVF == KVF_MX ? 4 : 1];            // MX: V scale byte per token j
+};
+
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void load_page_k(PageRaw<D, KVF>& r, const AttendArgs& a, uint32_t page,
+                                            uint32_t head, int g, int c) {
+    using R = PageRaw<D, KVF>;
+    constexpr int EB = R::FP8 ? 1 : 2;
+    const uint8_t* kp = a.kv + plane_offset(page, 0, head, a.hkv, D, EB);
+    #pragma unroll
+    for (int kb = 0; kb < R::KB; ++kb)
+        load_dwords<R::KW>(r.k[kb], kp + (c * D + kb * 32 + 8 * g) * EB);
+    if constexpr (KVF == KVF_MX) {
+        const uint8_t* s = reinterpret_cast<const uint8_t*>(a.scales) +
+                           ((uint64_t(page) * 2 + 0) * a.hkv + head) * uint64_t(kPageSize) * R::G;
+        #pragma unroll
+        for (int kb = 0; kb < R::G; ++kb) r.ksc[kb] = s[c * R::G + kb];
+    }
+}
+
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void load_page_v(PageRaw<D, KVF>& r, const AttendArgs& a, uint32_t page,
+                                            uint32_t head, int g, int c) {
+    using R = PageRaw<D, KVF>;
+    constexpr int EB = R::FP8 ? 1 : 2;
+    const uint8_t* vp = a.kv + plane_offset(page, 1, head, a.hkv, D, EB);
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+        load_dwords<R::VW>(r.v[j], vp + ((4 * g + j) * D + c * R::EPL) * EB);
+    if constexpr (KVF == KVF_MX) {
+        const uint8_t* s = reinterpret_cast<const uint8_t*>(a.scales) +
+                           ((uint64_t(page) * 2 + 1) * a.hkv + head) * uint64_t(kPageSize) * R::G;
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) r.vsc[j] = s[(4 * g + j) * R::G + (c * R::EPL) / 32];
+    }
+}
+
+// K rows of a page as MFMA A operands (bf16/f16 dwords).
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void k_operand(const PageRaw<D, KVF>& r, uint32_t (&op)[D / 32][4]) {
+    using R = PageRaw<D, KVF>;
+    #pragma unroll
+    for (int kb = 0; kb < R::KB; ++kb) {
+        if constexpr (!R::FP8) {
+            #pragma unroll
+            for (int w = 0; w < 4; ++w) op[kb][w] = r.k[kb][w];
+        } else {
+            const float sc = KVF == KVF_MX ? e8m0_to_float(r.ksc[kb]) : 1.f;
+            e4m3x4_to_bf16(r.k[kb][0], sc, op[kb][0], op[kb][1]);
+            e4m3x4_to_bf16(r.k[kb][1], sc, op[kb][2], op[kb][3]);
+        }
+    }
+}
+
+// V rows of a page (tokens 4g+j, dims c*EPL..) as bf16/f16 dwords; rows of
+// tokens at or beyond nt are zero so that garbage past the valid tokens can
+// never reach the accumulator (their probabilities are zero).
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void v_operand(const PageRaw<D, KVF>& r, int g, int nt,
+                                          uint32_t (&op)[4][D / 32]) {
+    using R = PageRaw<D, KVF>;
+    #pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool ok = 4 * g + j < nt;
+        if constexpr (!R::FP8) {
+            #pragma unroll
+            for (int w = 0; w < R::VW; ++w) op[j][w] = ok ? r.v[j][w] : 0u;
+        } else {
+            const float sc = KVF == KVF_MX ? e8m0_to_float(r.vsc[j]) : 1.f;
+            #pragma unroll
+            for (int w = 0; w < R::VW; ++w)
+                e4m3x4_to_bf16(ok ? r.v[j][w] : 0u, sc, op[j][2 * w], op[j][2 * w + 1]);
+        }
+    }
+}
+
+// The page loop of one wave for NRT row tiles (1 or 2), so the MFMA and
+// softmax sequences carry no per-tile branches.
+template <int D, uint32_t KVF, bool F16, int NRT, int RT>
+__device__ __forceinline__ void attend16_pages(const AttendArgs& a, const Item& it, uint32_t pb,
+                                               uint32_t pe, int g, int c,
+                                               const uint32_t (&qB)[RT][D / 32][4], float (&m)[RT],
+                                               float (&l)[RT], f4 (&O)[RT][D / 16]) {
+    constexpr int KB = D / 32;
+    constexpr int EPL = D / 16;
+    constexpr int VOW = EPL / 2;
+    constexpr bool BLOCK_SCALE = (KVF == KVF_FP8);
+    constexpr float kLazy = 8.f;                  // running-max slack (log2 units)
+
+    const int last_len = item_last_len(a, it);
+    const uint32_t* pages = a.pages + it.page_off;
+    const uint32_t head = it.kv_head;
+    const float* bsc = reinterpret_cast<const float*>(a.scales);
+
+    PageRaw<D, KVF> pr[2];
+    float ks[2] = {1.f, 1.f}, vs[2] = {1.f, 1.f};
+    {
+        uint32_t pg[2];
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t i = 2 * pb + p;
+            pg[p] = pages[i < it.npages ? i : it.npages - 1];
+        }
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            load_page_k<D, KVF>(pr[p], a, pg[p], head, g, c);
+            if constexpr (BLOCK_SCALE) ks[p] = bsc[(uint64_t(pg[p]) * 2 + 0) * a.hkv + head];
+        }
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            load_page_v<D, KVF>(pr[p], a, pg[p], head, g, c);
+            if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pg[p]) * 2 + 1) * a.hkv + head];
+        }
+    }
+
+    for (uint32_t pi = pb; pi < pe; ++pi) {
+        const uint32_t i0 = 2 * pi;
+        const int n0 = page_tokens(it, i0, last_len);
+        const int n1 = page_tokens(it, i0 + 1, last_len);
+        // Next pair's pages.  Past the end the loads repeat the last page:
+        // issuing them unconditionally keeps one load order on every path,
+        // so the wait before the next pair's scores covers K only.
+        uint32_t pgn[2];
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t i = i0 + 2 + p;
+            pgn[p] = pages[i < it.npages ? i : it.npages - 1];
+        }
+
+        // Scores of both pages for every row tile.
+        uint32_t kop[2][KB][4];
+        k_operand<D, KVF>(pr[0], kop[0]);
+        k_operand<D, KVF>(pr[1], kop[1]);
+        f4 s[NRT][2];
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            s[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
+            s[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                s[rt][0] = mma16<F16>(kop[0][kb], qB[rt][kb], s[rt][0]);
+                s[rt][1] = mma16<F16>(kop[1][kb], qB[rt][kb], s[rt][1]);
+            }
+        }
+        const float f0 = a.scale_log2 * ks[0], f1 = a.scale_log2 * ks[1];
+        const float v0s = vs[0], v1s = vs[1];
+        // K of the next pair is in flight behind the softmax and PV math.
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            load_page_k<D, KVF>(pr[p], a, pgn[p], head, g, c);
+            if constexpr (BLOCK_SCALE) ks[p] = bsc[(uint64_t(pgn[p]) * 2 + 0) * a.hkv + head];
+        }
+
+        // Online softmax per row tile -> probabilities as B operands.
+        uint32_t pB[NRT][4];
+        const bool full = (n0 == kPageSize) && (n1 == kPageSize);
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            float x0[4], x1[4];
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x0[i] = s[rt][0][i] * f0;
+                x1[i] = s[rt][1][i] * f1;
+            }
+            if (!full) {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (4 * g + i >= n0) x0[i] = kNegInf;
+                    if (4 * g + i >= n1) x1[i] = kNegInf;
+                }
+            }
+            float mx = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
+                             fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            // Lazy rescaling: the reference max only moves when a score
+            // exceeds it by more than kLazy, so exp2 stays <= 2^kLazy and the
+            // O/l rescale is skipped on most pairs (O / l is unchanged).
+            const bool need = mx > m[rt] + kLazy;
+            if (__ballot(need)) {
+                const float mnew = need ? mx : m[rt];
+                const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+                m[rt] = mnew;
+                l[rt] *= alpha;
+                #pragma unroll
+                for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
+            }
+            const float muse = (m[rt] == kNegInf) ? 0.f : m[rt];
+            float ps = 0.f;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x0[i] = fast_exp2(x0[i] - muse);
+                x1[i] = fast_exp2(x1[i] - muse);
+                ps += x0[i] + x1[i];
+            }
+            l[rt] += ps;
+            if constexpr (BLOCK_SCALE) {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x0[i] *= v0s;
+                    x1[i] *= v1s;
+                }
+            }
+            pB[rt][0] = pack2(x0[0], x0[1], F16);
+            pB[rt][1] = pack2(x0[2], x0[3], F16);
+            pB[rt][2] = pack2(x1[0], x1[1], F16);
+            pB[rt][3] = pack2(x1[2], x1[3], F16);
+        }
+
+        // O^T += V^T P^T over the pair; the V operand of a d-block is shared
+        // by all row tiles.
+        uint32_t vop[2][4][VOW];
+        v_operand<D, KVF>(pr[0], g, n0, vop[0]);
+        v_operand<D, KVF>(pr[1], g, n1, vop[1]);
+        #pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int w = e >> 1;
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            uint32_t vA[4];
+            vA[0] = __builtin_amdgcn_perm(vop[0][1][w], vop[0][0][w], sel);
+            vA[1] = __builtin_amdgcn_perm(vop[0][3][w], vop[0][2][w], sel);
+            vA[2] = __builtin_amdgcn_perm(vop[1][1][w], vop[1][0][w], sel);
+            vA[3] = __builtin_amdgcn_perm(vop[1][3][w], vop[1][2][w], sel);
+            #pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16<F16>(vA, pB[rt], O[rt][e]);
+        }
+        // V of the next pair.
+        #pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            load_page_v<D, KVF>(pr[p], a, pgn[p], head, g, c);
+            if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pgn[p]) * 2 + 1) * a.hkv + head];
+        }
+    }
+}
+
 template <int D, uint32_t KVF, bool F16>
-__global__ __launch_bounds__(256) void attend16_kernel(AttendArgs a) {
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendArgs a) {
     constexpr int KB = D / 32;                    // 32-dim k-chunks of a score tile
     constexpr int EPL = D / 16;                   // V elements per lane per token
     constexpr int RT = 2;                         // 16-row tiles per wave
-    constexpr bool FP8 = (KVF == KVF_FP8 || KVF == KVF_MX);
-    constexpr int EB = FP8 ? 1 : 2;               // element bytes in the pool
-    constexpr int VDW = EPL / 2;                  // bf16 dwords per lane per token
-    constexpr int G = D / 32;                     // MX groups per token
 
     __shared__ Combine<D, RT, EPL> sm;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    // Wave index as a wave-uniform (scalar) value: page-list reads then go
+    // through the scalar cache and never wait on the vector loads in flight.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const Item it = a.items[blockIdx.x];
     const int nrt = (int)((it.nrows + 15) >> 4);
-
-    for (int i = tid; i < RT * 16 * Combine<D, RT, EPL>::kStride; i += kWaves * 64) sm.o[i] = 0.f;
 
     // Query rows as B operands: lane (g, c) holds row c, dims kb*32 + 8g .. +8.
     uint32_t qB[RT][KB][4];
@@ -245,129 +504,11 @@ __global__ __launch_bounds__(256) void attend16_kernel(AttendArgs a) {
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int last_len = item_last_len(a, it);
     const uint32_t npairs = (it.npages + 1) >> 1;
     const uint32_t pb = (wave * npairs) / kWaves, pe = ((wave + 1) * npairs) / kWaves;
-    const uint32_t* pages = a.pages + it.page_off;
-    const uint64_t plane_bytes = uint64_t(kPageSize) * D * EB;
-
-    for (uint32_t pi = pb; pi < pe; ++pi) {
-        const uint32_t i0 = 2 * pi, i1 = i0 + 1;
-        const int n0 = page_tokens(it, i0, last_len);
-        const int n1 = page_tokens(it, i1, last_len);
-        const uint32_t pg[2] = {pages[i0], n1 > 0 ? pages[i1] : pages[i0]};
-        const int nt[2] = {n0, n1};
-
-        uint32_t kr[2][KB][4];   // K rows: token c, dims kb*32 + 8g .. +8 (bf16/f16)
-        uint32_t vr[2][4][VDW];  // V rows: token 4g+j, dims c*EPL .. +EPL (bf16/f16)
-        float ks[2] = {1.f, 1.f}, vs[2] = {1.f, 1.f};
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint8_t* kp = a.kv + plane_offset(pg[p], 0, it.kv_head, a.hkv, D, EB);
-            const uint8_t* vp = kp + uint64_t(a.hkv) * plane_bytes;
-            if constexpr (!FP8) {
-                #pragma unroll
-                for (int kb = 0; kb < KB; ++kb)
-                    load_dwords<4>(kr[p][kb], kp + (c * D + kb * 32 + 8 * g) * 2);
-                #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    load_dwords<VDW>(vr[p][j], vp + ((4 * g + j) * D + c * EPL) * 2);
-                    if (4 * g + j >= nt[p]) {
-                        #pragma unroll
-                        for (int w = 0; w < VDW; ++w) vr[p][j][w] = 0u;
-                    }
-                }
-            } else {
-                float kscale[KB], vscale[4];
-                if constexpr (KVF == KVF_FP8) {
-                    const float* sc = reinterpret_cast<const float*>(a.scales);
-                    ks[p] = sc[(uint64_t(pg[p]) * 2 + 0) * a.hkv + it.kv_head];
-                    vs[p] = sc[(uint64_t(pg[p]) * 2 + 1) * a.hkv + it.kv_head];
-                    #pragma unroll
-                    for (int kb = 0; kb < KB; ++kb) kscale[kb] = 1.f;
-                    #pragma unroll
-                    for (int j = 0; j < 4; ++j) vscale[j] = 1.f;
-                } else {
-                    const uint8_t* sb = reinterpret_cast<const uint8_t*>(a.scales);
-                    const uint64_t rec = uint64_t(kPageSize) * G;  // bytes per (page, plane, head)
-                    const uint8_t* skp = sb + ((uint64_t(pg[p]) * 2 + 0) * a.hkv + it.kv_head) * rec;
-                    const uint8_t* svp = sb + ((uint64_t(pg[p]) * 2 + 1) * a.hkv + it.kv_head) * rec;
-                    #pragma unroll
-                    for (int kb = 0; kb < KB; ++kb) kscale[kb] = e8m0_to_float(skp[c * G + kb]);
-                    #pragma unroll
-                    for (int j = 0; j < 4; ++j) vscale[j] = e8m0_to_float(svp[(4 * g + j) * G + (c * EPL) / 32]);
-                }
-                #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) {
-                    uint32_t raw[2];
-                    load_dwords<2>(raw, kp + c * D + kb * 32 + 8 * g);
-                    e4m3x4_to_bf16(raw[0], kscale[kb], kr[p][kb][0], kr[p][kb][1]);
-                    e4m3x4_to_bf16(raw[1], kscale[kb], kr[p][kb][2], kr[p][kb][3]);
-                }
-                #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t raw[EPL / 4];
-                    load_dwords<EPL / 4>(raw, vp + (4 * g + j) * D + c * EPL);
-                    const bool ok = 4 * g + j < nt[p];
-                    #pragma unroll
-                    for (int w = 0; w < EPL / 4; ++w) {
-                        e4m3x4_to_bf16(ok ? raw[w] : 0u, vscale[j], vr[p][j][2 * w], vr[p][j][2 * w + 1]);
-                    }
-                }
-            }
-        }
-
-        #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            if (rt >= nrt) break;
-            f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                s0 = mma16<F16>(kr[0][kb], qB[rt][kb], s0);
-                s1 = mma16<F16>(kr[1][kb], qB[rt][kb], s1);
-            }
-            const float f0 = a.scale_log2 * ks[0], f1 = a.scale_log2 * ks[1];
-            float x0[4], x1[4];
-            float mx = kNegInf;
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x0[i] = (4 * g + i < n0) ? s0[i] * f0 : kNegInf;
-                x1[i] = (4 * g + i < n1) ? s1[i] * f1 : kNegInf;
-                mx = fmaxf(mx, fmaxf(x0[i], x1[i]));
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(m[rt], mx);
-            const float muse = (mnew == kNegInf) ? 0.f : mnew;
-            const float alpha = fast_exp2(m[rt] - muse);
-            m[rt] = mnew;
-            float ps = 0.f;
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x0[i] = fast_exp2(x0[i] - muse);
-                x1[i] = fast_exp2(x1[i] - muse);
-                ps += x0[i] + x1[i];
-            }
-            l[rt] = l[rt] * alpha + ps;
-            #pragma unroll
-            for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
-            uint32_t pB[4];
-            pB[0] = pack2(x0[0] * vs[0], x0[1] * vs[0], F16);
-            pB[1] = pack2(x0[2] * vs[0], x0[3] * vs[0], F16);
-            pB[2] = pack2(x1[0] * vs[1], x1[1] * vs[1], F16);
-            pB[3] = pack2(x1[2] * vs[1], x1[3] * vs[1], F16);
-            #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int w = e >> 1;
-                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-                uint32_t vA[4];
-                vA[0] = __builtin_amdgcn_perm(vr[0][1][w], vr[0][0][w], sel);
-                vA[1] = __builtin_amdgcn_perm(vr[0][3][w], vr[0][2][w], sel);
-                vA[2] = __builtin_amdgcn_perm(vr[1][1][w], vr[1][0][w], sel);
-                vA[3] = __builtin_amdgcn_perm(vr[1][3][w], vr[1][2][w], sel);
-                O[rt][e] = mma16<F16>(vA, pB, O[rt][e]);
-            }
-        }
+    if (pb < pe) {
+        if (nrt == 2) attend16_pages<D, KVF, F16, 2, RT>(a, it, pb, pe, g, c, qB, m, l, O);
+        else attend16_pages<D, KVF, F16, 1, RT>(a, it, pb, pe, g, c, qB, m, l, O);
     }
 
     combine_and_store<D, RT, EPL>(a, it, sm, nrt, m, l, O);
@@ -388,8 +529,6 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const Item it = a.items[blockIdx.x];
     const int nrt = 1;
-
-    for (int i = tid; i < RT * 16 * Combine<D, RT, EPL>::kStride; i += kWaves * 64) sm.o[i] = 0.f;
 
     float qv[KQ];
     {

@@ -4,7 +4,7 @@
 #include <stdint.h>
 #include <string>
 
-#include "../../include/dendrite_hip.h"
+#include "dendrite_hip.h"
 
 namespace dh {
 

@@ -15,7 +15,7 @@
 #include <unordered_map>
 #include <unordered_set>
 
-#include "../../include/dendrite_hip.h"
+#include "dendrite_hip.h"
 
 namespace dh {
 namespace {

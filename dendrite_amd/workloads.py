@@ -262,4 +262,36 @@ def c5(seed: int = 0xC5, requests: int = 32, prefix_pages: int = 2048, beams: in
                                 f" {beams} beams + {suffix_pages * 16}-token suffixes, 64/8/128")
 
 
+def custom(tables, hq: int, hkv: int, d: int, q_dtype: int, kv_format: int, pool_pages: int,
+           last_page_len=None, seed: int = 0xD0, name: str = "custom", **kw) -> Workload:
+    """Any head shape / format over explicit page tables."""
+    ip, ix, lp = _csr([list(t) for t in tables], last_page_len)
+    return Workload(name, hq, hkv, d, q_dtype, kv_format, pool_pages, ip, ix, lp, seed, **kw)
+
+
+def random_tree(seed: int, hq: int, hkv: int, d: int, q_dtype: int, kv_format: int,
+                n_leaves: int = 12, pool_pages: int = 2048, max_depth: int = 4, max_run: int = 9,
+                partial: bool = True, **kw) -> Workload:
+    """Random fork tree: each node adds 0..max_run pages to its parent's table;
+    leaves optionally end on a partial page."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    perm = [int(x) for x in rng.permutation(pool_pages)]
+    nxt = [0]
+
+    def take(n):
+        out = perm[nxt[0]:nxt[0] + n]
+        nxt[0] += n
+        return out
+
+    tables = [take(int(rng.integers(0, max_run + 1)))]
+    while len(tables) < n_leaves:
+        parent = tables[int(rng.integers(0, len(tables)))]
+        tables.append(parent + take(int(rng.integers(0, max_run + 1))))
+        if rng.random() < 0.3 and len(tables[-1]) > 0:
+            tables[-1] = tables[-1][:int(rng.integers(0, len(tables[-1]) + 1))]
+    lpl = [int(rng.integers(1, 17)) if partial else 16 for _ in tables]
+    return custom(tables, hq, hkv, d, q_dtype, kv_format, pool_pages, lpl, seed=seed,
+                  name=f"tree{seed}", **kw)
+
+
 ALL = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}

@@ -72,3 +72,20 @@ def test_interleaved_gqa(backend):
     w = workloads.c2(branches=3, prefix_pages=12, suffix_pages=3, pool_pages=128)
     w.gqa_mapping = _lib.GQA_INTERLEAVED
     _check(w, backend)
+
+
+SHAPES = [(32, 4, 64), (32, 8, 128), (16, 2, 256), (8, 8, 128), (64, 8, 128)]
+FORMATS = [(_lib.DTYPE_BF16, _lib.KV_BF16), (_lib.DTYPE_F16, _lib.KV_F16),
+           (_lib.DTYPE_F32, _lib.KV_F32), (_lib.DTYPE_BF16, _lib.KV_FP8_E4M3),
+           (_lib.DTYPE_BF16, _lib.KV_MXFP8)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("fmt", FORMATS, ids=["bf16", "f16", "f32", "fp8", "mxfp8"])
+def test_random_trees(backend, shape, fmt):
+    """Random fork trees with partial last pages, every head shape and format,
+    cascade and flat plans."""
+    hq, hkv, d = shape
+    for seed in (11, 12):
+        w = workloads.random_tree(seed, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
+        _check(w, backend, cascade=(seed % 2 == 1))
