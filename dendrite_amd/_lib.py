@@ -60,6 +60,7 @@ class dh_plan_options(C.Structure):
 class dh_plan_stats(C.Structure):
     _fields_ = [("batch_size", C.c_uint32), ("num_segments", C.c_uint32),
                 ("num_shared_segments", C.c_uint32), ("num_items", C.c_uint32),
+                ("num_tasks", C.c_uint32), ("num_group_items", C.c_uint32),
                 ("num_partials", C.c_uint32), ("unique_pages", C.c_uint64),
                 ("page_reads", C.c_uint64), ("total_pages", C.c_uint64)]
 

@@ -21,8 +21,12 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}"]
-# Packed FP32 VALU forms are kept out of the generated code.
-DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Packed FP32 VALU forms are kept out of the generated code.  The kernels do
+# not rely on IEEE NaN semantics (inputs are finite; NaN inputs give NaN or
+# unspecified outputs), so the IEEE mode bit is off: fmax then needs no
+# operand canonicalisation.
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-fno-honor-nans", "-mno-amdgpu-ieee"]
 HOST = ["-D__HIP_PLATFORM_AMD__", f"-I{os.path.join(ROCM, 'include')}", "-x", "c++"]
 
 HIP_SOURCES = ["decode_kernels.hip"]

@@ -66,8 +66,10 @@ struct dh_plan {
     uint32_t batch;
     uint32_t pool_pages;
     uint32_t n_items;
+    uint32_t n_tasks;
     uint32_t n_slots;
     uint8_t* dev;
+    dh::Task* tasks;
     dh::Item* items;
     uint32_t* pages;
     dh::SeqSlot* seqslots;
@@ -380,7 +382,7 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     in.num_pool_pages = pool->num_pages;
     in.hq = cfg->num_heads;
     in.hkv = cfg->num_kv_heads;
-    in.rows_per_item = cfg->q_dtype == DH_DTYPE_F32 ? 16 : dh::kRowsPerItem;
+    in.wave_items_only = cfg->q_dtype == DH_DTYPE_F32;
     in.cascade = (flags & DH_PLAN_CASCADE) != 0;
     if (opt) {
         in.shared_chunk_pages = opt->shared_chunk_pages;
@@ -400,13 +402,16 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     pl->batch = batch;
     pl->pool_pages = pool->num_pages;
     pl->n_items = uint32_t(hp.items.size());
+    pl->n_tasks = uint32_t(hp.tasks.size());
     pl->n_slots = hp.num_slots;
-    const size_t o_items = 0;
+    const size_t o_tasks = 0;
+    const size_t o_items = align_up(o_tasks + hp.tasks.size() * sizeof(dh::Task), 256);
     const size_t o_pages = align_up(o_items + hp.items.size() * sizeof(dh::Item), 256);
     const size_t o_ss = align_up(o_pages + hp.pages.size() * sizeof(uint32_t), 256);
     const size_t o_sp = align_up(o_ss + hp.seqslots.size() * sizeof(dh::SeqSlot), 256);
     const size_t total = align_up(o_sp + hp.slot_ptr.size() * sizeof(uint32_t), 256);
     std::vector<uint8_t> blob(total, 0);
+    memcpy(blob.data() + o_tasks, hp.tasks.data(), hp.tasks.size() * sizeof(dh::Task));
     memcpy(blob.data() + o_items, hp.items.data(), hp.items.size() * sizeof(dh::Item));
     memcpy(blob.data() + o_pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
     memcpy(blob.data() + o_ss, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
@@ -419,6 +424,7 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
         delete pl;
         return fail(DH_EHIP, "plan upload failed: %s", hipGetErrorString(e));
     }
+    pl->tasks = reinterpret_cast<dh::Task*>(pl->dev + o_tasks);
     pl->items = reinterpret_cast<dh::Item*>(pl->dev + o_items);
     pl->pages = reinterpret_cast<uint32_t*>(pl->dev + o_pages);
     pl->seqslots = reinterpret_cast<dh::SeqSlot*>(pl->dev + o_ss);
@@ -430,6 +436,8 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     pl->stats.num_segments = hp.num_segments;
     pl->stats.num_shared_segments = hp.num_shared_segments;
     pl->stats.num_items = pl->n_items;
+    pl->stats.num_tasks = pl->n_tasks;
+    pl->stats.num_group_items = hp.num_group_items;
     pl->stats.num_partials = hp.num_slots;
     pl->stats.unique_pages = hp.unique_pages;
     pl->stats.page_reads = hp.page_reads;
@@ -479,6 +487,7 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
     float* ws_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
     if (mask & 1u) {
         dh::AttendArgs a;
+        a.tasks = pl->tasks;
         a.items = pl->items;
         a.pages = pl->pages;
         a.seqslots = pl->seqslots;
@@ -493,7 +502,7 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         a.r = c.num_heads / c.num_kv_heads;
         a.gqa_tiled = c.gqa_mapping == DH_GQA_TILED ? 1u : 0u;
         a.scale_log2 = c.scale * 1.4426950408889634f;
-        hipError_t e = hipError_t(dh::launch_attend(a, pl->n_items, c.q_dtype, c.kv_format, c.head_dim, stream));
+        hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     }
     if (mask & 2u) {

@@ -1,10 +1,16 @@
 // gfx950 (CDNA4) kernels of the paged tree-decode attention path.
 //
-// attend16 / attend32: one workgroup (four wave64s) per work item.  The item
-// names a run of 16-token pages, one KV head and up to 32 (16 for f32) query
-// rows; the four waves split the run's pages, each keeps an online softmax
-// for its rows, and the waves combine their states through LDS into one
-// partial state per row.  ReferenceBackend::decode (crates/dendrite-core/src/
+// attend16 / attend32: a workgroup of four wave64s runs one task, either
+//   - up to four wave items: each wave alone attends its item (<= 16 query
+//     rows, i.e. one sequence's GQA group of a private tail, or a few
+//     sequences of a small shared segment) over the item's pages, with the
+//     next page pair's loads in flight behind the current pair's math; or
+//   - one group item (<= 128 rows, a tree-shared prefix): every wave owns 32
+//     rows and all four consume the same page pairs, which the workgroup
+//     stages once into LDS (double-buffered, loads issued two pairs ahead),
+//     so a shared page is fetched once per 128 rows instead of once per wave.
+// Each wave keeps an online softmax for its rows and writes one partial
+// state per row.  ReferenceBackend::decode (crates/dendrite-core/src/
 // attention/backend.rs:206-265) computes softmax(q K^T * scale) V over the
 // concatenated pages; this is the same quantity, split over pages and merged
 // exactly by log-sum-exp.
@@ -44,6 +50,24 @@ constexpr uint32_t KVF_F16 = 0, KVF_BF16 = 1, KVF_F32 = 2, KVF_FP8 = 3, KVF_MX =
 constexpr float kNegInf = -__builtin_inff();
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Max over the four lanes l, l^16, l^32, l^48 (the four 16-lane rows of the
+// wave) with the gfx950 permlane swaps: after swap(x, x) the two results hold
+// x of the lane and of its partner row, so the max of the pair is the
+// xor-16 / xor-32 reduction without a trip through the LDS crossbar.
+__device__ __forceinline__ float rowgroup_max(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rowgroup_sum(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // Load n dwords (n in {1, 2, 4, 8}) from a naturally aligned address.
 template <int N>
@@ -86,6 +110,16 @@ __device__ __forceinline__ uint32_t pack2(float a, float b, bool f16) {
     return __builtin_bit_cast(uint32_t, t);
 }
 
+__device__ __forceinline__ float unpack_lo(uint32_t v, bool f16) {
+    if (f16) return float(__builtin_bit_cast(f16x2, v)[0]);
+    return __uint_as_float(v << 16);
+}
+
+__device__ __forceinline__ float unpack_hi(uint32_t v, bool f16) {
+    if (f16) return float(__builtin_bit_cast(f16x2, v)[1]);
+    return __uint_as_float(v & 0xFFFF0000u);
+}
+
 template <bool F16>
 __device__ __forceinline__ f4 mma16(const uint32_t* a, const uint32_t* b, f4 c) {
     u32x4 av = {a[0], a[1], a[2], a[3]};
@@ -117,103 +151,181 @@ __device__ __forceinline__ int page_tokens(const Item& it, uint32_t i, int last_
     return ((it.flags & kItemTail) && i + 1 == it.npages) ? last_len : kPageSize;
 }
 
+// Tokens in the item's last page.  Read through readfirstlane: the value is
+// wave-uniform, and telling the compiler so keeps every branch on the page
+// fill (full pair / partial pair) a scalar branch instead of a masked
+// execution of both sides.
 __device__ __forceinline__ int item_last_len(const AttendArgs& a, const Item& it) {
     if (!(it.flags & kItemTail) || a.last_page_len == nullptr) return kPageSize;
-    int L = a.last_page_len[it.tail_seq];
+    int L = __builtin_amdgcn_readfirstlane(a.last_page_len[it.tail_seq]);
     return (L <= 0 || L > kPageSize) ? kPageSize : L;
 }
 
-// Cross-wave combine.  Each wave holds, per row of its RT tiles of 16 rows,
-// (m, l_partial, O) with O[rt][e][i] = element d = (4g+i)*EPL + e of row
-// 16*rt + c.  The waves rescale their O to the workgroup's row maximum and
-// store it to their own LDS region; the sum over regions, divided by the
-// summed l, is the item's partial state.  (Plain stores: LDS float atomics
-// are far slower here.)
-template <int D, int RT, int EPL>
-struct Combine {
-    static constexpr int kStride = D + 4;
-    float o[kWaves][RT * 16 * kStride];
-    float m[kWaves][RT * 16];
-    float l[kWaves][RT * 16];
-    float inv[RT * 16];
-    uint32_t dst[RT * 16];
-};
-
-template <int D, int RT, int EPL, typename Smem>
-__device__ __forceinline__ void combine_and_store(const AttendArgs& a, const Item& it, Smem& sm,
-                                                  int nrt, float (&m)[RT], float (&l)[RT],
-                                                  f4 (&O)[RT][EPL]) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        float lt = l[rt] + __shfl_xor(l[rt], 16);
-        lt += __shfl_xor(lt, 32);
-        if (g == 0) {
-            sm.m[wave][rt * 16 + c] = rt < nrt ? m[rt] : kNegInf;
-            sm.l[wave][rt * 16 + c] = rt < nrt ? lt : 0.f;
-        }
-    }
-    __syncthreads();
+// Writes the partial states of one wave's rows: tiles rt < nrt, row
+// row0 + 16*rt + c of the item.  O[rt][e][i] is element d = (4g+i)*EPL + e.
+// lrow[rt]: the row's total weight when ROW_SUMMED, else this lane's share
+// (summed over the row's four lanes here).
+template <int D, int RT, bool ROW_SUMMED>
+__device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const Item& it, uint32_t row0,
+                                                   int nrt, const float (&m)[RT], const float (&lrow)[RT],
+                                                   const f4 (&O)[RT][D / 16], int g, int c) {
+    constexpr int EPL = D / 16;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         if (rt >= nrt) break;
-        const int row = rt * 16 + c;
-        float M = sm.m[0][row];
-        #pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm.m[w][row]);
-        if (m[rt] == kNegInf) continue;        // this wave saw no token: region unused
-        const float w8 = fast_exp2(m[rt] - M);
-        float* orow = sm.o[wave] + row * Smem::kStride;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        const float lt = ROW_SUMMED ? lrow[rt] : rowgroup_sum(lrow[rt]);
+        const uint32_t row = row0 + rt * kTileRows + c;
+        if (row < it.nrows) {
+            uint32_t seq, slot, qh;
+            row_target(a, it, row, seq, slot, qh);
+            const uint32_t dst = slot * a.hq + qh;
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            float* o = a.ws_o + uint64_t(dst) * D;
             #pragma unroll
-            for (int e = 0; e < EPL; e += 4) {
-                f4 v = {O[rt][e][i] * w8, O[rt][e + 1][i] * w8, O[rt][e + 2][i] * w8,
-                        O[rt][e + 3][i] * w8};
-                *reinterpret_cast<f4*>(orow + (4 * g + i) * EPL + e) = v;
+            for (int i = 0; i < 4; ++i) {
+                #pragma unroll
+                for (int e = 0; e < EPL; e += 4) {
+                    f4 v = {O[rt][e][i] * inv, O[rt][e + 1][i] * inv, O[rt][e + 2][i] * inv,
+                            O[rt][e + 3][i] * inv};
+                    *reinterpret_cast<f4*>(o + (4 * g + i) * EPL + e) = v;
+                }
             }
+            if (g == 0) a.ws_lse[dst] = lt > 0.f ? m[rt] + log2f(lt) : kNegInf;
         }
-    }
-    const int nrows = (int)it.nrows;
-    if (tid < nrows) {
-        float M = sm.m[0][tid];
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm.m[w][tid]);
-        float lt = 0.f;
-        if (M != kNegInf) {
-            for (int w = 0; w < kWaves; ++w) {
-                const float mw = sm.m[w][tid];
-                if (mw != kNegInf) lt += sm.l[w][tid] * fast_exp2(mw - M);
-            }
-        }
-        uint32_t seq, slot, qh;
-        row_target(a, it, tid, seq, slot, qh);
-        const uint32_t dst = slot * a.hq + qh;
-        a.ws_lse[dst] = lt > 0.f ? M + log2f(lt) : kNegInf;
-        sm.inv[tid] = lt > 0.f ? 1.f / lt : 0.f;
-        sm.dst[tid] = dst;
-    }
-    __syncthreads();
-    constexpr int Q4 = D / 4;
-    for (int idx = tid; idx < nrows * Q4; idx += kWaves * 64) {
-        const int row = idx / Q4, dq = idx - row * Q4;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            if (sm.m[w][row] == kNegInf) continue;
-            acc += *reinterpret_cast<const f4*>(sm.o[w] + row * Smem::kStride + 4 * dq);
-        }
-        *reinterpret_cast<f4*>(a.ws_o + uint64_t(sm.dst[row]) * D + 4 * dq) = acc * sm.inv[row];
     }
 }
 
-// ---------------------------------------------------------------- attend16
-// q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
-//
-// Each wave walks its pairs of pages with the loads of the next pair in
-// flight behind the current pair's math: K of pair i+1 is requested as soon
-// as the score MFMAs of pair i have consumed K, V of pair i+1 as soon as the
-// PV MFMAs have consumed V, so no extra registers hold a second buffer.
+// Query rows of NRT tiles as B operands: lane (g, c) holds row row0+16*rt+c,
+// dims kb*32 + 8g .. +8 (zero for rows outside the item).
+template <int D, int RT>
+__device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, uint32_t row0, int nrt,
+                                         uint32_t (&qB)[RT][D / 32][4], int g, int c) {
+    constexpr int KB = D / 32;
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint32_t row = row0 + rt * kTileRows + c;
+        if (rt < nrt && row < it.nrows) {
+            uint32_t seq, slot, qh;
+            row_target(a, it, row, seq, slot, qh);
+            const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
+        } else {
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) qB[rt][kb][0] = qB[rt][kb][1] = qB[rt][kb][2] = qB[rt][kb][3] = 0u;
+        }
+    }
+}
 
+// ---------------------------------------------------------------- pair math
+// Scores of a page pair for NRT row tiles: s[rt][p] = S^T tile of page p.
+template <int D, bool F16, int NRT, int RT>
+__device__ __forceinline__ void pair_scores(const uint32_t (&kop)[2][D / 32][4],
+                                            const uint32_t (&qB)[RT][D / 32][4], f4 (&s)[RT][2]) {
+    constexpr int KB = D / 32;
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        s[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
+        s[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            s[rt][0] = mma16<F16>(kop[0][kb], qB[rt][kb], s[rt][0]);
+            s[rt][1] = mma16<F16>(kop[1][kb], qB[rt][kb], s[rt][1]);
+        }
+    }
+}
+
+// Online softmax of a pair's scores and O^T += V^T P^T.  f0/f1: scale_log2
+// times the pages' K scales; v0s/v1s: the pages' V scales (1 unless FP8
+// block-scaled); n0/n1: valid tokens of the two pages (n1 = 0: no page).
+// vop holds, per page, the V rows of tokens 4g+j (bf16/f16 dwords, zero for
+// invalid tokens).
+//
+// Running max: a row's reference max m only moves when some score exceeds it
+// by more than kLazy (so every exp2 stays <= 2^kLazy).  Whether that happens
+// is decided from each lane's own scores and a ballot; the cross-lane max and
+// the O rescale run only then, which after the first pairs is rare.
+// Row sum: one more MFMA per tile multiplies the rounded probabilities by an
+// all-ones A operand, so L holds, in every lane of row c, the sum of exactly
+// the weights the PV MFMAs used (O / L is then a convex combination of V rows
+// whatever the rounding of P).
+template <int D, bool F16, int NRT, int RT, bool BLOCK_SCALE>
+__device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint32_t (&vop)[2][4][D / 32],
+                                                int n0, int n1, float f0, float f1, float v0s, float v1s,
+                                                float (&m)[RT], f4 (&L)[RT], f4 (&O)[RT][D / 16], int g) {
+    constexpr int EPL = D / 16;
+    constexpr float kLazy = 8.f;                  // running-max slack (log2 units)
+    const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
+    const uint32_t ones[4] = {one2, one2, one2, one2};
+    uint32_t pB[RT][4];
+    const bool full = (n0 == kPageSize) && (n1 == kPageSize);
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        float x0[4], x1[4];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x0[i] = s[rt][0][i];
+            x1[i] = s[rt][1][i];
+        }
+        if (!full) {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (4 * g + i >= n0) x0[i] = kNegInf;
+                if (4 * g + i >= n1) x1[i] = kNegInf;
+            }
+        }
+        // Lane-local max over raw scores (the scale factors are positive).
+        const float r0 = fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3]));
+        const float r1 = fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]));
+        const float lm = fmaxf(r0 * f0, r1 * f1);          // -inf * f stays -inf
+        if (__ballot(lm > m[rt] + kLazy)) {
+            const float mx = rowgroup_max(lm);
+            const float mnew = mx > m[rt] + kLazy ? mx : m[rt];
+            const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+            m[rt] = mnew;
+            L[rt] *= alpha;
+            #pragma unroll
+            for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
+        }
+        const float nm = (m[rt] == kNegInf) ? 0.f : -m[rt];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x0[i] = fast_exp2(__builtin_fmaf(x0[i], f0, nm));
+            x1[i] = fast_exp2(__builtin_fmaf(x1[i], f1, nm));
+        }
+        uint32_t pk[4];
+        pk[0] = pack2(x0[0], x0[1], F16);
+        pk[1] = pack2(x0[2], x0[3], F16);
+        pk[2] = pack2(x1[0], x1[1], F16);
+        pk[3] = pack2(x1[2], x1[3], F16);
+        L[rt] = mma16<F16>(ones, pk, L[rt]);
+        if constexpr (BLOCK_SCALE) {
+            pB[rt][0] = pack2(unpack_lo(pk[0], F16) * v0s, unpack_hi(pk[0], F16) * v0s, F16);
+            pB[rt][1] = pack2(unpack_lo(pk[1], F16) * v0s, unpack_hi(pk[1], F16) * v0s, F16);
+            pB[rt][2] = pack2(unpack_lo(pk[2], F16) * v1s, unpack_hi(pk[2], F16) * v1s, F16);
+            pB[rt][3] = pack2(unpack_lo(pk[3], F16) * v1s, unpack_hi(pk[3], F16) * v1s, F16);
+        } else {
+            #pragma unroll
+            for (int k = 0; k < 4; ++k) pB[rt][k] = pk[k];
+        }
+    }
+    // The V operand of a d-block (element e of the lane's 8 tokens) is
+    // shared by all row tiles.
+    #pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int w = e >> 1;
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t vA[4];
+        vA[0] = __builtin_amdgcn_perm(vop[0][1][w], vop[0][0][w], sel);
+        vA[1] = __builtin_amdgcn_perm(vop[0][3][w], vop[0][2][w], sel);
+        vA[2] = __builtin_amdgcn_perm(vop[1][1][w], vop[1][0][w], sel);
+        vA[3] = __builtin_amdgcn_perm(vop[1][3][w], vop[1][2][w], sel);
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16<F16>(vA, pB[rt], O[rt][e]);
+    }
+}
+
+// ------------------------------------------------------------- wave items
 // Raw pool bytes of one page for this lane (K rows of token c, V rows of
 // tokens 4g..4g+3), plus the MX scale bytes that go with them.
 template <int D, uint32_t KVF>
@@ -303,22 +415,30 @@ __device__ __forceinline__ void v_operand(const PageRaw<D, KVF>& r, int g, int n
     }
 }
 
-// The page loop of one wave for NRT row tiles (1 or 2), so the MFMA and
-// softmax sequences carry no per-tile branches.
-template <int D, uint32_t KVF, bool F16, int NRT, int RT>
-__device__ __forceinline__ void attend16_pages(const AttendArgs& a, const Item& it, uint32_t pb,
-                                               uint32_t pe, int g, int c,
-                                               const uint32_t (&qB)[RT][D / 32][4], float (&m)[RT],
-                                               float (&l)[RT], f4 (&O)[RT][D / 16]) {
-    constexpr int KB = D / 32;
+// One wave attends a wave item (one tile of <= 16 rows) over all its pages.
+// The next pair's K is requested as soon as the score MFMAs have consumed K,
+// its V as soon as the PV MFMAs have consumed V, so the loads of pair i+1 are
+// in flight behind the math of pair i without a second register buffer.
+// Past the end the loads repeat the last page: issuing them unconditionally
+// keeps one load order on every path, so the wait before a pair's scores
+// covers K only.
+template <int D, uint32_t KVF, bool F16>
+__device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, int g, int c) {
     constexpr int EPL = D / 16;
-    constexpr int VOW = EPL / 2;
+    constexpr int KB = D / 32;
     constexpr bool BLOCK_SCALE = (KVF == KVF_FP8);
-    constexpr float kLazy = 8.f;                  // running-max slack (log2 units)
+    uint32_t qB[1][KB][4];
+    load_q16<D, 1>(a, it, 0, 1, qB, g, c);
+    float m[1] = {kNegInf};
+    f4 L[1] = {f4{0.f, 0.f, 0.f, 0.f}};
+    f4 O[1][EPL];
+    #pragma unroll
+    for (int e = 0; e < EPL; ++e) O[0][e] = f4{0.f, 0.f, 0.f, 0.f};
 
     const int last_len = item_last_len(a, it);
     const uint32_t* pages = a.pages + it.page_off;
     const uint32_t head = it.kv_head;
+    const uint32_t np = it.npages;
     const float* bsc = reinterpret_cast<const float*>(a.scales);
 
     PageRaw<D, KVF> pr[2];
@@ -326,10 +446,7 @@ __device__ __forceinline__ void attend16_pages(const AttendArgs& a, const Item& 
     {
         uint32_t pg[2];
         #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t i = 2 * pb + p;
-            pg[p] = pages[i < it.npages ? i : it.npages - 1];
-        }
+        for (int p = 0; p < 2; ++p) pg[p] = pages[uint32_t(p) < np ? p : np - 1];
         #pragma unroll
         for (int p = 0; p < 2; ++p) {
             load_page_k<D, KVF>(pr[p], a, pg[p], head, g, c);
@@ -341,220 +458,329 @@ __device__ __forceinline__ void attend16_pages(const AttendArgs& a, const Item& 
             if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pg[p]) * 2 + 1) * a.hkv + head];
         }
     }
-
-    for (uint32_t pi = pb; pi < pe; ++pi) {
+    const uint32_t npairs = (np + 1) >> 1;
+    for (uint32_t pi = 0; pi < npairs; ++pi) {
         const uint32_t i0 = 2 * pi;
         const int n0 = page_tokens(it, i0, last_len);
         const int n1 = page_tokens(it, i0 + 1, last_len);
-        // Next pair's pages.  Past the end the loads repeat the last page:
-        // issuing them unconditionally keeps one load order on every path,
-        // so the wait before the next pair's scores covers K only.
         uint32_t pgn[2];
         #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const uint32_t i = i0 + 2 + p;
-            pgn[p] = pages[i < it.npages ? i : it.npages - 1];
+            pgn[p] = pages[i < np ? i : np - 1];
         }
-
-        // Scores of both pages for every row tile.
         uint32_t kop[2][KB][4];
         k_operand<D, KVF>(pr[0], kop[0]);
         k_operand<D, KVF>(pr[1], kop[1]);
-        f4 s[NRT][2];
-        #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            s[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
-            s[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                s[rt][0] = mma16<F16>(kop[0][kb], qB[rt][kb], s[rt][0]);
-                s[rt][1] = mma16<F16>(kop[1][kb], qB[rt][kb], s[rt][1]);
-            }
-        }
+        f4 s[1][2];
+        pair_scores<D, F16, 1, 1>(kop, qB, s);
         const float f0 = a.scale_log2 * ks[0], f1 = a.scale_log2 * ks[1];
         const float v0s = vs[0], v1s = vs[1];
-        // K of the next pair is in flight behind the softmax and PV math.
         #pragma unroll
         for (int p = 0; p < 2; ++p) {
             load_page_k<D, KVF>(pr[p], a, pgn[p], head, g, c);
             if constexpr (BLOCK_SCALE) ks[p] = bsc[(uint64_t(pgn[p]) * 2 + 0) * a.hkv + head];
         }
-
-        // Online softmax per row tile -> probabilities as B operands.
-        uint32_t pB[NRT][4];
+        uint32_t vop[2][4][D / 32];
         const bool full = (n0 == kPageSize) && (n1 == kPageSize);
-        #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            float x0[4], x1[4];
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x0[i] = s[rt][0][i] * f0;
-                x1[i] = s[rt][1][i] * f1;
-            }
-            if (!full) {
-                #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (4 * g + i >= n0) x0[i] = kNegInf;
-                    if (4 * g + i >= n1) x1[i] = kNegInf;
-                }
-            }
-            float mx = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
-                             fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            // Lazy rescaling: the reference max only moves when a score
-            // exceeds it by more than kLazy, so exp2 stays <= 2^kLazy and the
-            // O/l rescale is skipped on most pairs (O / l is unchanged).
-            const bool need = mx > m[rt] + kLazy;
-            if (__ballot(need)) {
-                const float mnew = need ? mx : m[rt];
-                const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
-                m[rt] = mnew;
-                l[rt] *= alpha;
-                #pragma unroll
-                for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
-            }
-            const float muse = (m[rt] == kNegInf) ? 0.f : m[rt];
-            float ps = 0.f;
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x0[i] = fast_exp2(x0[i] - muse);
-                x1[i] = fast_exp2(x1[i] - muse);
-                ps += x0[i] + x1[i];
-            }
-            l[rt] += ps;
-            if constexpr (BLOCK_SCALE) {
-                #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    x0[i] *= v0s;
-                    x1[i] *= v1s;
-                }
-            }
-            pB[rt][0] = pack2(x0[0], x0[1], F16);
-            pB[rt][1] = pack2(x0[2], x0[3], F16);
-            pB[rt][2] = pack2(x1[0], x1[1], F16);
-            pB[rt][3] = pack2(x1[2], x1[3], F16);
+        if (full) {
+            v_operand<D, KVF>(pr[0], g, kPageSize, vop[0]);
+            v_operand<D, KVF>(pr[1], g, kPageSize, vop[1]);
+        } else {
+            v_operand<D, KVF>(pr[0], g, n0, vop[0]);
+            v_operand<D, KVF>(pr[1], g, n1, vop[1]);
         }
-
-        // O^T += V^T P^T over the pair; the V operand of a d-block is shared
-        // by all row tiles.
-        uint32_t vop[2][4][VOW];
-        v_operand<D, KVF>(pr[0], g, n0, vop[0]);
-        v_operand<D, KVF>(pr[1], g, n1, vop[1]);
-        #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const int w = e >> 1;
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            uint32_t vA[4];
-            vA[0] = __builtin_amdgcn_perm(vop[0][1][w], vop[0][0][w], sel);
-            vA[1] = __builtin_amdgcn_perm(vop[0][3][w], vop[0][2][w], sel);
-            vA[2] = __builtin_amdgcn_perm(vop[1][1][w], vop[1][0][w], sel);
-            vA[3] = __builtin_amdgcn_perm(vop[1][3][w], vop[1][2][w], sel);
-            #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16<F16>(vA, pB[rt], O[rt][e]);
-        }
-        // V of the next pair.
+        pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(s, vop, n0, n1, f0, f1, v0s, v1s, m, L, O, g);
         #pragma unroll
         for (int p = 0; p < 2; ++p) {
             load_page_v<D, KVF>(pr[p], a, pgn[p], head, g, c);
             if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pgn[p]) * 2 + 1) * a.hkv + head];
         }
     }
+    const float lr[1] = {L[0][0]};
+    write_wave_partial<D, 1, true>(a, it, 0, 1, m, lr, O, g, c);
+}
+
+// ------------------------------------------------------------ group items
+// LDS stage of one page pair: planes K(page 0), K(page 1), V(page 0),
+// V(page 1), each 16 rows with a 16-byte pad per row (bank spread), then the
+// four MX scale records.
+template <int D, uint32_t KVF>
+struct GroupLayout {
+    static constexpr bool FP8 = (KVF == KVF_FP8 || KVF == KVF_MX);
+    static constexpr int EB = FP8 ? 1 : 2;
+    static constexpr int RB = D * EB;               // row bytes
+    static constexpr int RS = RB + 16;              // LDS row stride
+    static constexpr int PLANE = kPageSize * RS;
+    static constexpr int G = D / 32;
+    static constexpr int SREC = kPageSize * G;      // MX scale record bytes
+    static constexpr int STAGE = 4 * PLANE + (KVF == KVF_MX ? 4 * SREC : 0);
+    static constexpr int CPP = kPageSize * RB / 16; // 16-byte chunks per plane
+    static constexpr int NCH = 4 * CPP / (kWaves * 64);   // chunks per thread per pair
+    static constexpr int NSC = (KVF == KVF_MX) ? 4 * SREC / 4 : 0;   // scale dwords per pair
+    static_assert(NCH >= 1 && (4 * CPP) % (kWaves * 64) == 0, "pair must split evenly");
+    static_assert(NSC <= kWaves * 64, "scale records must fit one dword per thread");
+};
+
+template <int D, uint32_t KVF>
+struct Staged {
+    uint32_t d[GroupLayout<D, KVF>::NCH][4];
+    uint32_t sc;
+};
+
+// Issues the global loads of page pair `pair` of the item into registers.
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void group_issue(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                            uint32_t pair, Staged<D, KVF>& st, int tid) {
+    using L = GroupLayout<D, KVF>;
+    const uint32_t np = it.npages;
+    const uint32_t i0 = 2 * pair;
+    const uint32_t p0 = ids[i0 < np ? i0 : np - 1];
+    const uint32_t p1 = ids[i0 + 1 < np ? i0 + 1 : np - 1];
+    #pragma unroll
+    for (int u = 0; u < L::NCH; ++u) {
+        const int q = tid + u * kWaves * 64;
+        const int plane = q / L::CPP, within = q - plane * L::CPP;
+        const uint32_t page = (plane & 1) ? p1 : p0;
+        const uint8_t* src = a.kv + plane_offset(page, plane >> 1, it.kv_head, a.hkv, D, L::EB) + within * 16;
+        load_dwords<4>(st.d[u], src);
+    }
+    if constexpr (KVF == KVF_MX) {
+        if (tid < L::NSC) {
+            const int rec = tid / (L::SREC / 4), w = tid - rec * (L::SREC / 4);
+            const uint32_t page = (rec & 1) ? p1 : p0;
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(a.scales) +
+                                 ((uint64_t(page) * 2 + (rec >> 1)) * a.hkv + it.kv_head) * L::SREC + 4 * w;
+            st.sc = *reinterpret_cast<const uint32_t*>(src);
+        }
+    }
+}
+
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void group_commit(uint8_t* stage, const Staged<D, KVF>& st, int tid) {
+    using L = GroupLayout<D, KVF>;
+    #pragma unroll
+    for (int u = 0; u < L::NCH; ++u) {
+        const int q = tid + u * kWaves * 64;
+        const int plane = q / L::CPP, within = q - plane * L::CPP;
+        const int row = within / (L::RB / 16), col = within - row * (L::RB / 16);
+        u32x4 v = {st.d[u][0], st.d[u][1], st.d[u][2], st.d[u][3]};
+        *reinterpret_cast<u32x4*>(stage + plane * L::PLANE + row * L::RS + col * 16) = v;
+    }
+    if constexpr (KVF == KVF_MX) {
+        if (tid < L::NSC) *reinterpret_cast<uint32_t*>(stage + 4 * L::PLANE + 4 * tid) = st.sc;
+    }
+}
+
+// Reads one wave's K / V operands of a staged pair from LDS.
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void group_operands(const uint8_t* stage, int g, int c, int n0, int n1,
+                                               uint32_t (&kop)[2][D / 32][4],
+                                               uint32_t (&vop)[2][4][D / 32]) {
+    using L = GroupLayout<D, KVF>;
+    constexpr int KB = D / 32, EPL = D / 16;
+    #pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const uint8_t* kp = stage + p * L::PLANE + c * L::RS;
+        #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            if constexpr (!L::FP8) {
+                load_dwords<4>(kop[p][kb], kp + (kb * 32 + 8 * g) * 2);
+            } else {
+                uint32_t raw[2];
+                load_dwords<2>(raw, kp + kb * 32 + 8 * g);
+                float sc = 1.f;
+                if constexpr (KVF == KVF_MX) sc = e8m0_to_float(stage[4 * L::PLANE + p * L::SREC + c * L::G + kb]);
+                e4m3x4_to_bf16(raw[0], sc, kop[p][kb][0], kop[p][kb][1]);
+                e4m3x4_to_bf16(raw[1], sc, kop[p][kb][2], kop[p][kb][3]);
+            }
+        }
+    }
+    #pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int nt = p ? n1 : n0;
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * g + j;
+            const uint8_t* vp = stage + (2 + p) * L::PLANE + tok * L::RS + c * EPL * L::EB;
+            const bool ok = tok < nt;
+            if constexpr (!L::FP8) {
+                uint32_t raw[EPL / 2];
+                load_dwords<EPL / 2>(raw, vp);
+                #pragma unroll
+                for (int w = 0; w < EPL / 2; ++w) vop[p][j][w] = ok ? raw[w] : 0u;
+            } else {
+                uint32_t raw[EPL / 4];
+                load_dwords<EPL / 4>(raw, vp);
+                float sc = 1.f;
+                if constexpr (KVF == KVF_MX)
+                    sc = e8m0_to_float(stage[4 * L::PLANE + (2 + p) * L::SREC + tok * L::G + (c * EPL) / 32]);
+                #pragma unroll
+                for (int w = 0; w < EPL / 4; ++w)
+                    e4m3x4_to_bf16(ok ? raw[w] : 0u, sc, vop[p][j][2 * w], vop[p][j][2 * w + 1]);
+            }
+        }
+    }
+}
+
+// The group item's pair loop for a wave owning NRT tiles (NRT = 0: the
+// wave's rows are all outside the item; it still stages pages and joins
+// every barrier).  Two LDS stages; global loads run two pairs ahead in two
+// register sets A and B (loop unrolled by two so the sets never move).
+template <int D, uint32_t KVF, bool F16, int NRT, int RT>
+__device__ __forceinline__ void group_loop(const AttendArgs& a, const Item& it, uint8_t* lds,
+                                           const uint32_t* ids, const float* bscale, int tid,
+                                           int g, int c, const uint32_t (&qB)[RT][D / 32][4],
+                                           float (&m)[RT], f4 (&Lsum)[RT], f4 (&O)[RT][D / 16]) {
+    using L = GroupLayout<D, KVF>;
+    constexpr bool BLOCK_SCALE = (KVF == KVF_FP8);
+    const int last_len = item_last_len(a, it);
+    const uint32_t np = it.npages;
+    const uint32_t npairs = (np + 1) >> 1;
+    uint8_t* stage0 = lds;
+    uint8_t* stage1 = lds + L::STAGE;
+
+    auto compute = [&](const uint8_t* stage, uint32_t pair) {
+        if constexpr (NRT > 0) {
+            const uint32_t i0 = 2 * pair;
+            const int n0 = page_tokens(it, i0, last_len);
+            const int n1 = page_tokens(it, i0 + 1, last_len);
+            float f0 = a.scale_log2, f1 = a.scale_log2, v0s = 1.f, v1s = 1.f;
+            if constexpr (BLOCK_SCALE) {
+                const uint32_t i1 = i0 + 1 < np ? i0 + 1 : i0;
+                f0 *= bscale[2 * i0];
+                f1 *= bscale[2 * i1];
+                v0s = bscale[2 * i0 + 1];
+                v1s = bscale[2 * i1 + 1];
+            }
+            uint32_t kop[2][D / 32][4];
+            uint32_t vop[2][4][D / 32];
+            group_operands<D, KVF>(stage, g, c, n0, n1, kop, vop);
+            f4 s[RT][2];
+            pair_scores<D, F16, NRT, RT>(kop, qB, s);
+            pair_softmax_pv<D, F16, NRT, RT, BLOCK_SCALE>(s, vop, n0, n1, f0, f1, v0s, v1s, m, Lsum, O, g);
+        }
+    };
+
+    Staged<D, KVF> A, B;
+    group_issue<D, KVF>(a, it, ids, 0, A, tid);
+    group_issue<D, KVF>(a, it, ids, 1, B, tid);
+    group_commit<D, KVF>(stage0, A, tid);
+    group_issue<D, KVF>(a, it, ids, 2, A, tid);
+    __syncthreads();
+    for (uint32_t pi = 0; pi < npairs; pi += 2) {
+        compute(stage0, pi);
+        group_commit<D, KVF>(stage1, B, tid);      // pair pi+1
+        group_issue<D, KVF>(a, it, ids, pi + 3, B, tid);
+        __syncthreads();
+        if (pi + 1 >= npairs) break;
+        compute(stage1, pi + 1);
+        group_commit<D, KVF>(stage0, A, tid);      // pair pi+2
+        group_issue<D, KVF>(a, it, ids, pi + 4, A, tid);
+        __syncthreads();
+    }
 }
 
 template <int D, uint32_t KVF, bool F16>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendArgs a) {
-    constexpr int KB = D / 32;                    // 32-dim k-chunks of a score tile
-    constexpr int EPL = D / 16;                   // V elements per lane per token
-    constexpr int RT = 2;                         // 16-row tiles per wave
-
-    __shared__ Combine<D, RT, EPL> sm;
-
-    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
-    // Wave index as a wave-uniform (scalar) value: page-list reads then go
-    // through the scalar cache and never wait on the vector loads in flight.
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const Item it = a.items[blockIdx.x];
-    const int nrt = (int)((it.nrows + 15) >> 4);
-
-    // Query rows as B operands: lane (g, c) holds row c, dims kb*32 + 8g .. +8.
-    uint32_t qB[RT][KB][4];
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const uint32_t row = rt * 16 + c;
-        if (rt < nrt && row < it.nrows) {
-            uint32_t seq, slot, qh;
-            row_target(a, it, row, seq, slot, qh);
-            const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
-        } else {
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) qB[rt][kb][0] = qB[rt][kb][1] = qB[rt][kb][2] = qB[rt][kb][3] = 0u;
+__device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, uint8_t* lds, int tid,
+                                           int wave, int g, int c) {
+    constexpr int RT = kGroupTiles;
+    constexpr int EPL = D / 16;
+    constexpr int KB = D / 32;
+    // The item's page ids (and FP8 block scales) go to LDS once, so the pair
+    // loop reads them without a vector load, whose wait would also drain the
+    // page loads running ahead.
+    uint32_t* ids = reinterpret_cast<uint32_t*>(lds + 2 * GroupLayout<D, KVF>::STAGE);
+    float* bscale = reinterpret_cast<float*>(ids + kGroupMaxPages);
+    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) {
+        const uint32_t pg = a.pages[it.page_off + i];
+        ids[i] = pg;
+        if constexpr (KVF == KVF_FP8) {
+            const float* bsc = reinterpret_cast<const float*>(a.scales);
+            bscale[2 * i] = bsc[(uint64_t(pg) * 2 + 0) * a.hkv + it.kv_head];
+            bscale[2 * i + 1] = bsc[(uint64_t(pg) * 2 + 1) * a.hkv + it.kv_head];
         }
     }
-
-    float m[RT], l[RT];
+    __syncthreads();
+    const uint32_t row0 = uint32_t(wave) * RT * kTileRows;
+    const int nrt = it.nrows > row0 ? min(RT, int((it.nrows - row0 + kTileRows - 1) / kTileRows)) : 0;
+    uint32_t qB[RT][KB][4];
+    load_q16<D, RT>(a, it, row0, nrt, qB, g, c);
+    float m[RT];
+    f4 L[RT];
     f4 O[RT][EPL];
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         m[rt] = kNegInf;
-        l[rt] = 0.f;
+        L[rt] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    if (nrt == RT) group_loop<D, KVF, F16, RT, RT>(a, it, lds, ids, bscale, tid, g, c, qB, m, L, O);
+    else if (nrt == 1) group_loop<D, KVF, F16, 1, RT>(a, it, lds, ids, bscale, tid, g, c, qB, m, L, O);
+    else group_loop<D, KVF, F16, 0, RT>(a, it, lds, ids, bscale, tid, g, c, qB, m, L, O);
+    float lr[RT];
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) lr[rt] = L[rt][0];
+    write_wave_partial<D, RT, true>(a, it, row0, nrt, m, lr, O, g, c);
+}
 
-    const uint32_t npairs = (it.npages + 1) >> 1;
-    const uint32_t pb = (wave * npairs) / kWaves, pe = ((wave + 1) * npairs) / kWaves;
-    if (pb < pe) {
-        if (nrt == 2) attend16_pages<D, KVF, F16, 2, RT>(a, it, pb, pe, g, c, qB, m, l, O);
-        else attend16_pages<D, KVF, F16, 1, RT>(a, it, pb, pe, g, c, qB, m, l, O);
+// ---------------------------------------------------------------- attend16
+// q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
+template <int D, uint32_t KVF, bool F16>
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * GroupLayout<D, KVF>::STAGE +
+                                                        kGroupMaxPages * 4 * (KVF == KVF_FP8 ? 3 : 1)];
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    // Wave index as a wave-uniform (scalar) value: page-list reads then go
+    // through the scalar cache and never wait on the vector loads in flight.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const Task t = a.tasks[blockIdx.x];
+    if (t.kind == kTaskGroup) {
+        const Item it = a.items[t.first];
+        group_item<D, KVF, F16>(a, it, lds, tid, wave, g, c);
+    } else if (uint32_t(wave) < t.count) {
+        const Item it = a.items[t.first + wave];
+        wave_item<D, KVF, F16>(a, it, g, c);
     }
-
-    combine_and_store<D, RT, EPL>(a, it, sm, nrt, m, l, O);
 }
 
 // ---------------------------------------------------------------- attend32
-// f32 q and f32 KV: v_mfma_f32_16x16x4_f32, one page per step, 16 rows.
+// f32 q and f32 KV (wave items only): v_mfma_f32_16x16x4_f32, one page per
+// step, 16 rows per wave.
 //   S^T: A = K[token c][g*D/4 + kb], B = Q[row c][g*D/4 + kb], kb < D/4.
 //   O^T: for token group i: A = V[4g+i][c*EPL + e], B = P[row c][4g+i].
 template <int D>
 __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     constexpr int KQ = D / 4;
     constexpr int EPL = D / 16;
-    constexpr int RT = 1;
-
-    __shared__ Combine<D, RT, EPL> sm;
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
-    const Item it = a.items[blockIdx.x];
-    const int nrt = 1;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const Task t = a.tasks[blockIdx.x];
+    if (uint32_t(wave) >= t.count) return;
+    const Item it = a.items[t.first + wave];
 
     float qv[KQ];
-    {
-        const uint32_t row = c;
-        if (row < it.nrows) {
-            uint32_t seq, slot, qh;
-            row_target(a, it, row, seq, slot, qh);
-            const float* qp = reinterpret_cast<const float*>(a.q) + (uint64_t(seq) * a.hq + qh) * D + g * KQ;
-            load_dwords<KQ>(reinterpret_cast<uint32_t*>(qv), qp);
-        } else {
-            #pragma unroll
-            for (int k = 0; k < KQ; ++k) qv[k] = 0.f;
-        }
+    if (uint32_t(c) < it.nrows) {
+        uint32_t seq, slot, qh;
+        row_target(a, it, c, seq, slot, qh);
+        const float* qp = reinterpret_cast<const float*>(a.q) + (uint64_t(seq) * a.hq + qh) * D + g * KQ;
+        load_dwords<KQ>(reinterpret_cast<uint32_t*>(qv), qp);
+    } else {
+        #pragma unroll
+        for (int k = 0; k < KQ; ++k) qv[k] = 0.f;
     }
 
-    float m[RT] = {kNegInf}, l[RT] = {0.f};
-    f4 O[RT][EPL];
+    float m[1] = {kNegInf}, l[1] = {0.f};
+    f4 O[1][EPL];
     #pragma unroll
     for (int e = 0; e < EPL; ++e) O[0][e] = f4{0.f, 0.f, 0.f, 0.f};
 
     const int last_len = item_last_len(a, it);
-    const uint32_t pb = (wave * it.npages) / kWaves, pe = ((wave + 1) * it.npages) / kWaves;
     const uint32_t* pages = a.pages + it.page_off;
     const uint64_t plane_bytes = uint64_t(kPageSize) * D * 4;
 
-    for (uint32_t pi = pb; pi < pe; ++pi) {
+    for (uint32_t pi = 0; pi < it.npages; ++pi) {
         const int n0 = page_tokens(it, pi, last_len);
         const uint8_t* kp = a.kv + plane_offset(pages[pi], 0, it.kv_head, a.hkv, D, 4);
         const uint8_t* vp = kp + uint64_t(a.hkv) * plane_bytes;
@@ -579,8 +805,7 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
             x[i] = (4 * g + i < n0) ? s[i] * a.scale_log2 : kNegInf;
             mx = fmaxf(mx, x[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = rowgroup_max(mx);
         const float mnew = fmaxf(m[0], mx);
         const float muse = (mnew == kNegInf) ? 0.f : mnew;
         const float alpha = fast_exp2(m[0] - muse);
@@ -601,8 +826,7 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
                 O[0][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i][e], x[i], O[0][e], 0, 0, 0);
         }
     }
-
-    combine_and_store<D, RT, EPL>(a, it, sm, nrt, m, l, O);
+    write_wave_partial<D, 1, false>(a, it, 0, 1, m, l, O, g, c);
 }
 
 // ------------------------------------------------------------------ merge

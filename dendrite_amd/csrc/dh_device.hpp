@@ -1,12 +1,11 @@
 // Structures shared by the host planner/launcher and the gfx950 kernels.
 //
-// A decode step is cut into work items.  One item is attended by one
-// workgroup of four wave64s: a run of pages (all 16-token pages of one chunk
-// of a segment), one KV head and up to 32 query rows.  A segment is either a
-// run of pages shared by several sequences (a tree-shared prefix, the CoW
-// sharing TreeState::fork creates, crates/dendrite-core/src/tree/state.rs:
-// 49-84) or one sequence's private tail.  Every item writes one partial
-// attention state (O normalised, log2-sum-exp) per query row into the
+// A decode step is cut into work items.  A segment is either a run of pages
+// shared by several sequences (a tree-shared prefix, the CoW sharing
+// TreeState::fork creates, crates/dendrite-core/src/tree/state.rs:49-84) or
+// one sequence's private tail; an item is one chunk of a segment's pages, one
+// KV head and a block of the segment's query rows.  Every item writes one
+// partial attention state (O normalised, log2-sum-exp) per query row into the
 // workspace; the merge kernel combines the partial states of each
 // (sequence, query head) by log-sum-exp into the output.
 #pragma once
@@ -22,21 +21,37 @@
 namespace dh {
 
 constexpr int kPageSize = 16;       // tokens per page (dendrite-ffi flashinfer/mod.rs:14)
-constexpr int kWaves = 4;           // wave64s per attention workgroup
-constexpr int kRowsPerItem = 32;    // query rows per item (two 16-row MFMA tiles)
+constexpr int kWaves = 4;           // wave64s per workgroup
+constexpr int kTileRows = 16;       // query rows of one MFMA tile
+constexpr int kWaveRows = 16;       // rows of a wave item: one tile, one wave
+constexpr int kGroupTiles = 1;      // tiles per wave in a group item
+constexpr int kGroupRows = kWaves * kGroupTiles * kTileRows;   // 64
+constexpr int kGroupMaxPages = 256; // pages of one group item (LDS page-id list)
 
-// One attention work item (32 bytes, read once per workgroup).
+// One attention work item (32 bytes): a run of pages of one segment chunk,
+// one KV head and a block of query rows.
 struct Item {
     uint32_t page_off;   // first page of the item in Plan::pages
     uint32_t npages;     // pages in the item (>= 1)
     uint32_t seq_off;    // first SeqSlot of the item's (segment, chunk)
     uint32_t row_begin;  // first row; row rho -> seq_local = rho / r, j = rho % r
-    uint32_t nrows;      // rows in the item, 1..kRowsPerItem
+    uint32_t nrows;      // rows in the item
     uint32_t kv_head;
     uint32_t flags;      // kItemTail: the item's last page is tail_seq's last page
     uint32_t tail_seq;
 };
 constexpr uint32_t kItemTail = 1u;
+
+// What one workgroup does: up to four wave items (one per wave, <= 16 rows
+// each) or one group item (<= 128 rows: each wave owns 32 rows and all four
+// waves read the same pages, staged once in LDS).
+struct Task {
+    uint32_t kind;       // kTaskWaves or kTaskGroup
+    uint32_t first;      // first item
+    uint32_t count;      // items (1 for a group task)
+    uint32_t pad;
+};
+constexpr uint32_t kTaskWaves = 0u, kTaskGroup = 1u;
 
 // Sequence of a (segment, chunk) and the partial-state slot it owns there.
 struct SeqSlot {
@@ -45,6 +60,7 @@ struct SeqSlot {
 };
 
 struct AttendArgs {
+    const Task* tasks;
     const Item* items;
     const uint32_t* pages;
     const SeqSlot* seqslots;
@@ -79,7 +95,7 @@ DH_HOST_DEVICE inline uint64_t plane_offset(uint32_t page, uint32_t plane, uint3
 // Kernel launchers (defined in decode_kernels.hip).  Return hipError_t as int.
 extern "C++" {
 namespace dh {
-int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint32_t kv_format,
+int launch_attend(const AttendArgs& a, uint32_t n_tasks, uint32_t q_dtype, uint32_t kv_format,
                   uint32_t head_dim, void* stream);
 int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t head_dim, void* stream);
 int launch_merge_states(const float* o_a, const float* lse_a, const float* o_b,

@@ -50,7 +50,6 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         return DH_EINVAL;
     }
     const uint32_t r = in.hq / in.hkv;
-    const uint32_t rpi = in.rows_per_item;
 
     // 1. Page lists with INVALID entries dropped (ReferenceBackend::decode
     //    skips blocks it has no KV for, attention/backend.rs:228-233).
@@ -153,30 +152,42 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     }
     out.num_segments = uint32_t(segs.size());
 
-    // 3. Chunk sizes.  A chunk is the page run of one item; its four waves
-    //    split it.  More chunks mean more parallelism and more partial states.
-    uint32_t shared_chunk = in.shared_chunk_pages ? in.shared_chunk_pages : 64;
-    uint32_t private_chunk = in.private_chunk_pages ? in.private_chunk_pages : 64;
-    const uint32_t target = in.target_items ? in.target_items : 1024;
-    auto count_items = [&](uint32_t sc, uint32_t pc) {
+    // 3. Item classes and chunk sizes.  A segment with at most kWaveRows
+    //    query rows becomes wave items (one wave each); a larger one becomes
+    //    group items of up to kGroupRows rows whose four waves share every
+    //    page through LDS.  Chunks split a segment's pages over items: more
+    //    chunks give more parallelism and more partial states.
+    auto is_group = [&](const Segment& sg) {
+        return !in.wave_items_only && uint32_t(sg.seqs.size()) * r > uint32_t(kWaveRows);
+    };
+    uint32_t group_chunk = std::min<uint32_t>(in.shared_chunk_pages ? in.shared_chunk_pages : 64,
+                                              kGroupMaxPages);
+    uint32_t wave_chunk = in.private_chunk_pages ? in.private_chunk_pages : 32;
+    const uint32_t target = in.target_items ? in.target_items : 1536;   // waves
+    auto count_waves = [&](uint32_t gc, uint32_t wc) {
         uint64_t n = 0;
-        for (const auto& s : segs) {
-            const uint32_t ch = s.tail ? pc : sc;
-            const uint32_t rows = uint32_t(s.seqs.size()) * r;
-            n += uint64_t(ceil_div(uint32_t(s.pages.size()), ch)) * ceil_div(rows, rpi) * in.hkv;
+        for (const auto& sg : segs) {
+            const uint32_t rows = uint32_t(sg.seqs.size()) * r;
+            if (is_group(sg)) {
+                n += uint64_t(ceil_div(uint32_t(sg.pages.size()), gc)) * ceil_div(rows, kGroupRows) *
+                     in.hkv * kWaves;
+            } else {
+                n += uint64_t(ceil_div(uint32_t(sg.pages.size()), wc)) * ceil_div(rows, kWaveRows) * in.hkv;
+            }
         }
         return n;
     };
-    while (count_items(shared_chunk, private_chunk) < target && (shared_chunk > 8 || private_chunk > 8)) {
-        if (shared_chunk > 8) shared_chunk /= 2;
-        if (private_chunk > 8) private_chunk /= 2;
+    while (count_waves(group_chunk, wave_chunk) < target && (group_chunk > 8 || wave_chunk > 4)) {
+        if (wave_chunk > 4) wave_chunk /= 2;
+        if (count_waves(group_chunk, wave_chunk) >= target) break;
+        if (group_chunk > 8) group_chunk /= 2;
     }
 
     // 4. Partial-state slots: one per (segment chunk, sequence), contiguous
     //    per sequence.
     std::vector<uint32_t> nchunks(segs.size());
     for (size_t s = 0; s < segs.size(); ++s) {
-        const uint32_t ch = segs[s].tail ? private_chunk : shared_chunk;
+        const uint32_t ch = is_group(segs[s]) ? group_chunk : wave_chunk;
         nchunks[s] = ceil_div(uint32_t(segs[s].pages.size()), ch);
     }
     out.slot_ptr.assign(B + 1, 0);
@@ -188,11 +199,13 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     out.num_slots = out.slot_ptr[B];
     std::vector<uint32_t> cursor(out.slot_ptr.begin(), out.slot_ptr.end() - 1);
 
-    // 5. Items, grouped by the pages they read.
-    std::vector<Group> groups;
+    // 5. Items.  Group items that read the same pages are kept together.
+    std::vector<Group> groups;      // group items by (segment, chunk, head)
+    std::vector<std::pair<double, Item>> waves;
     std::unordered_set<uint32_t> uniq;
     for (size_t s = 0; s < segs.size(); ++s) {
         const Segment& sg = segs[s];
+        const bool grp = is_group(sg);
         const uint32_t np = uint32_t(sg.pages.size());
         const uint32_t base = uint32_t(out.pages.size());
         out.pages.insert(out.pages.end(), sg.pages.begin(), sg.pages.end());
@@ -200,66 +213,86 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         out.page_reads += np;
         const uint32_t nc = nchunks[s];
         const uint32_t rows = uint32_t(sg.seqs.size()) * r;
-        const uint32_t nrb = ceil_div(rows, rpi);
+        const uint32_t block = grp ? uint32_t(kGroupRows) : uint32_t(kWaveRows);
+        const uint32_t nrb = ceil_div(rows, block);
         for (uint32_t ci = 0; ci < nc; ++ci) {
             const uint32_t p0 = uint32_t(uint64_t(ci) * np / nc);
             const uint32_t p1 = uint32_t(uint64_t(ci + 1) * np / nc);
             const uint32_t seq_off = uint32_t(out.seqslots.size());
             for (uint32_t b : sg.seqs) out.seqslots.push_back(SeqSlot{b, cursor[b]++});
             for (uint32_t h = 0; h < in.hkv; ++h) {
-                Group grp;
+                Group gr;
                 for (uint32_t rb = 0; rb < nrb; ++rb) {
                     Item it;
                     it.page_off = base + p0;
                     it.npages = p1 - p0;
                     it.seq_off = seq_off;
-                    it.row_begin = rb * rpi;
-                    it.nrows = std::min(rpi, rows - rb * rpi);
+                    it.row_begin = rb * block;
+                    it.nrows = std::min(block, rows - rb * block);
                     it.kv_head = h;
-                    const bool last = sg.tail && ci + 1 == nc;
-                    it.flags = last ? kItemTail : 0u;
+                    it.flags = (sg.tail && ci + 1 == nc) ? kItemTail : 0u;
                     it.tail_seq = sg.tail ? sg.seqs[0] : 0u;
-                    grp.cost += double(it.npages) * (2.0 + ceil_div(it.nrows, 16));
-                    grp.items.push_back(it);
+                    const double cost = double(it.npages) * (2.0 + ceil_div(it.nrows, kTileRows));
+                    if (grp) {
+                        gr.items.push_back(it);
+                        gr.cost += cost;
+                    } else {
+                        waves.emplace_back(cost, it);
+                    }
                 }
-                groups.push_back(std::move(grp));
+                if (grp) groups.push_back(std::move(gr));
             }
         }
     }
     out.unique_pages = uniq.size();
 
-    // 6. Order: heaviest groups first; the items of one group land on the
-    //    same XCD (workgroups are dispatched round-robin over the 8 XCDs, so
-    //    indices congruent mod 8 share an L2) to reuse the group's pages in L2.
+    // 6. Tasks.  Heaviest first.  Group tasks that read the same pages land
+    //    on the same XCD (workgroups are dispatched round-robin over the 8
+    //    XCDs, so task indices congruent mod 8 share an L2).  Wave items are
+    //    packed four to a task, heaviest together.
     std::stable_sort(groups.begin(), groups.end(),
-                     [](const Group& a, const Group& b) { return a.cost > b.cost; });
+                     [](const Group& x, const Group& y) { return x.cost > y.cost; });
+    std::stable_sort(waves.begin(), waves.end(),
+                     [](const std::pair<double, Item>& x, const std::pair<double, Item>& y) {
+                         return x.first > y.first;
+                     });
     constexpr int kXcds = 8;
     std::vector<std::vector<Item>> q(kXcds);
     std::vector<double> qcost(kXcds, 0.0);
-    for (auto& grp : groups) {
+    for (auto& gr : groups) {
         int best = 0;
         for (int x = 1; x < kXcds; ++x)
-            if (qcost[x] < qcost[best] ||
-                (qcost[x] == qcost[best] && q[x].size() < q[best].size()))
+            if (qcost[x] < qcost[best] || (qcost[x] == qcost[best] && q[x].size() < q[best].size()))
                 best = x;
-        for (auto& it : grp.items) q[best].push_back(it);
-        qcost[best] += grp.cost;
+        for (auto& it : gr.items) q[best].push_back(it);
+        qcost[best] += gr.cost;
     }
+    std::vector<Item> gorder;
     size_t total = 0;
     for (auto& v : q) total += v.size();
-    out.items.reserve(total);
     std::vector<size_t> pos(kXcds, 0);
-    while (out.items.size() < total) {
+    while (gorder.size() < total) {
         bool all = true;
         for (int x = 0; x < kXcds; ++x)
             if (pos[x] >= q[x].size()) all = false;
         if (all) {
-            for (int x = 0; x < kXcds; ++x) out.items.push_back(q[x][pos[x]++]);
+            for (int x = 0; x < kXcds; ++x) gorder.push_back(q[x][pos[x]++]);
         } else {
             for (int x = 0; x < kXcds; ++x)
-                while (pos[x] < q[x].size()) out.items.push_back(q[x][pos[x]++]);
+                while (pos[x] < q[x].size()) gorder.push_back(q[x][pos[x]++]);
         }
     }
+    for (const Item& it : gorder) {
+        out.tasks.push_back(Task{kTaskGroup, uint32_t(out.items.size()), 1u, 0u});
+        out.items.push_back(it);
+    }
+    for (size_t i = 0; i < waves.size(); i += kWaves) {
+        const uint32_t n = uint32_t(std::min<size_t>(kWaves, waves.size() - i));
+        out.tasks.push_back(Task{kTaskWaves, uint32_t(out.items.size()), n, 0u});
+        for (uint32_t k = 0; k < n; ++k) out.items.push_back(waves[i + k].second);
+    }
+    out.num_group_items = uint32_t(gorder.size());
+    out.num_wave_items = uint32_t(waves.size());
     return DH_OK;
 }
 

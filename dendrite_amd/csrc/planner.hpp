@@ -13,7 +13,7 @@ struct PlanInput {
     const uint32_t* indices = nullptr;  // [indptr[batch]]
     uint32_t num_pool_pages = 0;
     uint32_t hq = 0, hkv = 0;
-    uint32_t rows_per_item = kRowsPerItem;
+    bool wave_items_only = false;       // f32: every item is a <= 16-row wave item
     bool cascade = true;
     uint32_t shared_chunk_pages = 0;    // 0 = default
     uint32_t private_chunk_pages = 0;
@@ -21,11 +21,14 @@ struct PlanInput {
 };
 
 struct HostPlan {
+    std::vector<Task> tasks;
     std::vector<Item> items;
     std::vector<uint32_t> pages;
     std::vector<SeqSlot> seqslots;
     std::vector<uint32_t> slot_ptr;     // [batch + 1]
     uint32_t num_slots = 0;
+    uint32_t num_group_items = 0;
+    uint32_t num_wave_items = 0;
     uint32_t num_segments = 0;
     uint32_t num_shared_segments = 0;
     uint64_t unique_pages = 0;

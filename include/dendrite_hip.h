@@ -224,7 +224,9 @@ typedef struct dh_plan_stats {
     uint32_t batch_size;
     uint32_t num_segments;        /* shared runs + private tails              */
     uint32_t num_shared_segments;
-    uint32_t num_items;           /* attention work items (one wave each)     */
+    uint32_t num_items;           /* attention work items                     */
+    uint32_t num_tasks;           /* workgroups of the attention launch       */
+    uint32_t num_group_items;     /* items whose pages four waves share       */
     uint32_t num_partials;        /* partial states per q head                */
     uint64_t unique_pages;        /* distinct pages read per step             */
     uint64_t page_reads;          /* pages read per step summed over items of
