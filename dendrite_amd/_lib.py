@@ -65,6 +65,11 @@ class dh_plan_stats(C.Structure):
                 ("page_reads", C.c_uint64), ("total_pages", C.c_uint64)]
 
 
+class dh_plan_item(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("page_off", "npages", "seq_off", "row_begin", "nrows",
+                                          "kv_head", "flags", "tail_seq")]
+
+
 class dh_node_info(C.Structure):
     _fields_ = [("id", C.c_uint64), ("parent", C.c_uint64), ("num_tokens", C.c_uint64),
                 ("num_children", C.c_uint32), ("is_active", C.c_uint32)]
@@ -105,6 +110,8 @@ SIGNATURES = {
     "dh_plan_destroy": (_I, [_P]),
     "dh_plan_workspace_size": (C.c_size_t, [_P]),
     "dh_plan_get_stats": (_I, [_P, C.POINTER(dh_plan_stats)]),
+    "dh_plan_inspect": (_I, [_P, _U32, _PU32, _PU32, _U32, _U32, _P, C.POINTER(dh_plan_stats), _P, _PU32,
+                             _PU32, _PU32, _PU32, _PU32]),
     "dh_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "dh_decode_stages": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _U32, _P]),
     "dh_merge_states": (_I, [_P, _P, _P, _P, _P, _P, _U32, _U32, _P]),

@@ -242,6 +242,37 @@ class DecodePlan:
                            device=f"cuda:{self.backend.device}")
 
 
+def plan_inspect(config: AttentionConfig, num_pool_pages: int, indptr, indices, cascade: bool = True,
+                 shared_chunk_pages: int = 0, private_chunk_pages: int = 0,
+                 target_items: int = 0) -> dict:
+    """Host-only planning (dh_plan_inspect): the plan's stats, items, page list
+    and (sequence, slot) pairs, without a device."""
+    ip = np.ascontiguousarray(indptr, dtype=np.uint32)
+    ix = np.ascontiguousarray(indices, dtype=np.uint32)
+    batch = len(ip) - 1
+    opt = _lib.dh_plan_options()
+    opt.shared_chunk_pages = shared_chunk_pages
+    opt.private_chunk_pages = private_chunk_pages
+    opt.target_items = target_items
+    c = config.to_c()
+    flags = _lib.PLAN_CASCADE if cascade else _lib.PLAN_FLAT
+    ni, npg, nss = C.c_uint32(), C.c_uint32(), C.c_uint32()
+    st = _lib.dh_plan_stats()
+    args = (C.byref(c), num_pool_pages, ip.ctypes.data_as(_lib._PU32),
+            ix.ctypes.data_as(_lib._PU32) if len(ix) else None, batch, flags, C.byref(opt))
+    check(lib().dh_plan_inspect(*args, C.byref(st), None, C.byref(ni), None, C.byref(npg), None,
+                                C.byref(nss)))
+    items = (_lib.dh_plan_item * max(1, ni.value))()
+    pages = np.zeros(max(1, npg.value), dtype=np.uint32)
+    ss = np.zeros(2 * max(1, nss.value), dtype=np.uint32)
+    check(lib().dh_plan_inspect(*args, C.byref(st), items, C.byref(ni), pages.ctypes.data_as(_lib._PU32),
+                                C.byref(npg), ss.ctypes.data_as(_lib._PU32), C.byref(nss)))
+    fields = [f for f, _ in _lib.dh_plan_item._fields_]
+    return {"stats": {k: getattr(st, k) for k, _ in st._fields_},
+            "items": [{f: getattr(items[i], f) for f in fields} for i in range(ni.value)],
+            "pages": pages[:npg.value], "seqslots": ss[:2 * nss.value].reshape(-1, 2)}
+
+
 def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream=None,
                  stages: int = 3) -> None:
     """One decode step through dh_decode_stages (stages=3 is dh_decode_batch).

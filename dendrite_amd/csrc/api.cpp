@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <new>
 #include <string>
 #include <vector>
@@ -42,15 +43,64 @@ int launch_scatter(uint8_t* dst, const uint8_t* src, const uint32_t* ids, uint32
 
 using dh::fail;
 
+// A failed HIP call also leaves the runtime's per-thread last error set,
+// where the caller's next hipGetLastError (torch checks it after every
+// launch) would find it; the error is reported through dh_status instead.
 #define DH_HIP(expr)                                                                      \
     do {                                                                                  \
         hipError_t e_ = (expr);                                                           \
-        if (e_ != hipSuccess) return fail(DH_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+        if (e_ != hipSuccess) {                                                           \
+            (void)hipGetLastError();                                                      \
+            return fail(DH_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));          \
+        }                                                                                 \
     } while (0)
 
+namespace dh {
+
+// Makes `device` current for the scope and restores the caller's device.
+class DeviceGuard {
+public:
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        err_ = (prev_ == device) ? hipSuccess : hipSetDevice(device);
+        if (err_ != hipSuccess) (void)hipGetLastError();
+        set_ = (err_ == hipSuccess && prev_ >= 0 && prev_ != device);
+    }
+    ~DeviceGuard() {
+        if (set_) (void)hipSetDevice(prev_);
+    }
+    hipError_t error() const { return err_; }
+    DeviceGuard(const DeviceGuard&) = delete;
+    DeviceGuard& operator=(const DeviceGuard&) = delete;
+
+private:
+    int prev_ = -1;
+    hipError_t err_ = hipSuccess;
+    bool set_ = false;
+};
+
+}  // namespace dh
+
+#define DH_DEVICE(dev)                                                                    \
+    dh::DeviceGuard device_guard_(dev);                                                   \
+    if (device_guard_.error() != hipSuccess)                                              \
+    return fail(DH_EHIP, "hipSetDevice(%d) failed: %s", int(dev), hipGetErrorString(device_guard_.error()))
+
+// Pools and plans keep their backend alive: a handle may be destroyed in any
+// order relative to the objects made from it.
 struct dh_backend {
     int device;
+    std::atomic<int> refs;
 };
+
+static dh_backend* retain(dh_backend* be) {
+    be->refs.fetch_add(1, std::memory_order_relaxed);
+    return be;
+}
+
+static void release(dh_backend* be) {
+    if (be && be->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) delete be;
+}
 
 struct dh_pool {
     dh_backend* be;
@@ -117,8 +167,8 @@ static dh_status validate_config(const dh_attn_config* cfg) {
     // batch_decode.rs:33-39, flashinfer/mod.rs:20
     if (cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256)
         return fail(DH_EINVAL, "unsupported head_dim: %u, supported: [64, 128, 256]", cfg->head_dim);
-    if (cfg->sliding_window != 0)
-        return fail(DH_EUNSUPPORTED, "sliding_window is not supported (no Dendrite backend reads it)");
+    // sliding_window is ignored, as ReferenceBackend::decode ignores it
+    // (attention/backend.rs:206-265 never reads the field).
     if (cfg->gqa_mapping > DH_GQA_INTERLEAVED) return fail(DH_EINVAL, "bad gqa_mapping %u", cfg->gqa_mapping);
     if (cfg->q_dtype > DH_DTYPE_F32) return fail(DH_EINVAL, "bad q_dtype %u", cfg->q_dtype);
     if (cfg->kv_format > DH_KV_MXFP8) return fail(DH_EINVAL, "bad kv_format %u", cfg->kv_format);
@@ -154,7 +204,6 @@ dh_status dh_create(int device, dh_backend** out) {
     if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
         return fail(DH_EUNSUPPORTED, "no HIP device available");
     if (device < 0 || device >= n) return fail(DH_EINVAL, "device %d out of range (%d devices)", device, n);
-    DH_HIP(hipSetDevice(device));
     hipDeviceProp_t prop;
     DH_HIP(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
@@ -163,25 +212,26 @@ dh_status dh_create(int device, dh_backend** out) {
     dh_backend* be = new (std::nothrow) dh_backend;
     if (!be) return fail(DH_ENOMEM, "out of host memory");
     be->device = device;
+    be->refs.store(1, std::memory_order_relaxed);
     *out = be;
     return DH_OK;
 }
 
 dh_status dh_destroy(dh_backend* be) {
-    delete be;
+    release(be);
     return DH_OK;
 }
 
 dh_status dh_memory_info(dh_backend* be, size_t* free_b, size_t* total_b) {
     if (!be || !free_b || !total_b) return fail(DH_EINVAL, "NULL argument");
-    DH_HIP(hipSetDevice(be->device));
+    DH_DEVICE(be->device);
     DH_HIP(hipMemGetInfo(free_b, total_b));
     return DH_OK;
 }
 
 dh_status dh_synchronize(dh_backend* be) {
     if (!be) return fail(DH_EINVAL, "backend is NULL");
-    DH_HIP(hipSetDevice(be->device));
+    DH_DEVICE(be->device);
     DH_HIP(hipDeviceSynchronize());
     return DH_OK;
 }
@@ -197,7 +247,7 @@ dh_status dh_pool_create(dh_backend* be, uint32_t num_pages, uint32_t hkv, uint3
     if (d != 64 && d != 128 && d != 256) return fail(DH_EINVAL, "unsupported head_dim: %u", d);
     const uint32_t eb = dh::kv_elem_bytes(fmt);
     if (eb == 0) return fail(DH_EINVAL, "bad kv_format %u", fmt);
-    DH_HIP(hipSetDevice(be->device));
+    DH_DEVICE(be->device);
     dh_pool* p = new (std::nothrow) dh_pool;
     if (!p) return fail(DH_ENOMEM, "out of host memory");
     p->be = be;
@@ -210,11 +260,12 @@ dh_status dh_pool_create(dh_backend* be, uint32_t num_pages, uint32_t hkv, uint3
     p->scale_bytes = dh::kv_scale_bytes(fmt, hkv, d);
     p->data = nullptr;
     p->scales = nullptr;
-    hipError_t e = hipMalloc(&p->data, p->page_bytes * num_pages);
+    const unsigned long long data_bytes = (unsigned long long)(p->page_bytes * num_pages);
+    hipError_t e = hipMalloc(&p->data, data_bytes);
     if (e != hipSuccess) {
+        (void)hipGetLastError();
         delete p;
-        return fail(DH_ENOMEM, "pool allocation of %llu bytes failed: %s",
-                    (unsigned long long)(p->page_bytes * num_pages), hipGetErrorString(e));
+        return fail(DH_ENOMEM, "pool allocation of %llu bytes failed: %s", data_bytes, hipGetErrorString(e));
     }
     e = hipMemset(p->data, 0, p->page_bytes * num_pages);
     if (e == hipSuccess && p->scale_bytes) {
@@ -222,21 +273,27 @@ dh_status dh_pool_create(dh_backend* be, uint32_t num_pages, uint32_t hkv, uint3
         if (e == hipSuccess) e = hipMemset(p->scales, 0, p->scale_bytes * num_pages);
     }
     if (e != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(p->data);
         if (p->scales) (void)hipFree(p->scales);
         delete p;
         return fail(DH_ENOMEM, "pool initialisation failed: %s", hipGetErrorString(e));
     }
+    retain(be);
     *out = p;
     return DH_OK;
 }
 
 dh_status dh_pool_destroy(dh_pool* p) {
     if (!p) return DH_OK;
-    (void)hipSetDevice(p->be->device);
-    (void)hipDeviceSynchronize();
-    (void)hipFree(p->data);
-    if (p->scales) (void)hipFree(p->scales);
+    {
+        dh::DeviceGuard g(p->be->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p->data);
+        if (p->scales) (void)hipFree(p->scales);
+        (void)hipGetLastError();
+    }
+    release(p->be);
     delete p;
     return DH_OK;
 }
@@ -257,7 +314,7 @@ dh_status dh_pool_write_tokens(dh_pool* p, uint32_t page_id, uint32_t tok_offset
                     tok_offset + n_tok, DH_PAGE_SIZE);
     if ((p->fmt == DH_KV_FP8_E4M3 || p->fmt == DH_KV_MXFP8) && (!k_scale || !v_scale))
         return fail(DH_EINVAL, "scales are required for this kv format");
-    DH_HIP(hipSetDevice(p->be->device));
+    DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint64_t row = uint64_t(p->d) * p->eb;
     for (uint32_t plane = 0; plane < 2; ++plane) {
@@ -296,7 +353,7 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
     for (uint32_t i = 0; i < n; ++i)
         if (ids[i] >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", ids[i]);
     if (n == 0) return DH_OK;
-    DH_HIP(hipSetDevice(p->be->device));
+    DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint32_t batch = std::min<uint32_t>(n, std::max<uint64_t>(1, (256ull << 20) / p->page_bytes));
     uint8_t* stage = nullptr;
@@ -331,7 +388,7 @@ dh_status dh_pool_copy_page(dh_pool* p, uint32_t src, uint32_t dst, void* stream
     if (src >= p->num_pages || dst >= p->num_pages)
         return fail(DH_EINVAL, "page id outside the pool (src %u, dst %u)", src, dst);
     if (src == dst) return DH_OK;
-    DH_HIP(hipSetDevice(p->be->device));
+    DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     DH_HIP(hipMemcpyAsync(p->data + uint64_t(dst) * p->page_bytes, p->data + uint64_t(src) * p->page_bytes,
                           p->page_bytes, hipMemcpyDeviceToDevice, s));
@@ -345,7 +402,7 @@ dh_status dh_pool_copy_page(dh_pool* p, uint32_t src, uint32_t dst, void* stream
 dh_status dh_pool_read_page(dh_pool* p, uint32_t page_id, void* data_out, void* scales_out) {
     if (!p || !data_out) return fail(DH_EINVAL, "NULL argument");
     if (page_id >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", page_id);
-    DH_HIP(hipSetDevice(p->be->device));
+    DH_DEVICE(p->be->device);
     DH_HIP(hipDeviceSynchronize());
     DH_HIP(hipMemcpy(data_out, p->data + uint64_t(page_id) * p->page_bytes, p->page_bytes,
                      hipMemcpyDeviceToHost));
@@ -359,27 +416,21 @@ dh_status dh_pool_read_page(dh_pool* p, uint32_t page_id, void* data_out, void* 
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
-                         const uint32_t* indptr, const uint32_t* indices, uint32_t batch,
-                         uint32_t flags, const dh_plan_options* opt, dh_plan** out) {
-    if (!be || !pool || !out) return fail(DH_EINVAL, "NULL argument");
-    *out = nullptr;
+// Validates the planning inputs and runs the host planner.
+static dh_status host_plan(const dh_attn_config* cfg, uint32_t num_pool_pages, const uint32_t* indptr,
+                           const uint32_t* indices, uint32_t batch, uint32_t flags,
+                           const dh_plan_options* opt, dh::HostPlan& hp) {
     dh_status st = validate_config(cfg);
     if (st != DH_OK) return st;
-    if (pool->hkv != cfg->num_kv_heads || pool->d != cfg->head_dim || pool->fmt != cfg->kv_format)
-        return fail(DH_EINVAL, "pool (kv heads %u, head_dim %u, format %u) does not match the config "
-                    "(%u, %u, %u)", pool->hkv, pool->d, pool->fmt, cfg->num_kv_heads, cfg->head_dim,
-                    cfg->kv_format);
     if (batch && !indptr) return fail(DH_EINVAL, "indptr is NULL");
     if (batch && indptr[batch] > indptr[0] && !indices) return fail(DH_EINVAL, "indices is NULL");
     if (flags & ~DH_PLAN_CASCADE) return fail(DH_EINVAL, "unknown plan flags 0x%x", flags);
-
     dh::PlanInput in;
     in.batch = batch;
-    std::vector<uint32_t> zero_ptr(1, 0);
-    in.indptr = batch ? indptr : zero_ptr.data();
+    static const uint32_t zero_ptr[1] = {0};
+    in.indptr = batch ? indptr : zero_ptr;
     in.indices = indices;
-    in.num_pool_pages = pool->num_pages;
+    in.num_pool_pages = num_pool_pages;
     in.hq = cfg->num_heads;
     in.hkv = cfg->num_kv_heads;
     in.wave_items_only = cfg->q_dtype == DH_DTYPE_F32;
@@ -389,10 +440,68 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
         in.private_chunk_pages = opt->private_chunk_pages;
         in.target_items = opt->target_items;
     }
-    dh::HostPlan hp;
     std::string err;
-    int rc = dh::build_plan(in, hp, err);
+    const int rc = dh::build_plan(in, hp, err);
     if (rc != DH_OK) return fail(dh_status(rc), "%s", err.c_str());
+    return DH_OK;
+}
+
+static void fill_stats(const dh::HostPlan& hp, uint32_t batch, dh_plan_stats* s) {
+    memset(s, 0, sizeof *s);
+    s->batch_size = batch;
+    s->num_segments = hp.num_segments;
+    s->num_shared_segments = hp.num_shared_segments;
+    s->num_items = uint32_t(hp.items.size());
+    s->num_tasks = uint32_t(hp.tasks.size());
+    s->num_group_items = hp.num_group_items;
+    s->num_partials = hp.num_slots;
+    s->unique_pages = hp.unique_pages;
+    s->page_reads = hp.page_reads;
+    s->total_pages = hp.total_pages;
+}
+
+dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages, const uint32_t* indptr,
+                          const uint32_t* indices, uint32_t batch, uint32_t flags,
+                          const dh_plan_options* opt, dh_plan_stats* stats, dh_plan_item* items,
+                          uint32_t* n_items, uint32_t* pages, uint32_t* n_pages, uint32_t* seqslots,
+                          uint32_t* n_seqslots) {
+    if (!n_items || !n_pages || !n_seqslots) return fail(DH_EINVAL, "NULL size argument");
+    dh::HostPlan hp;
+    dh_status st = host_plan(cfg, num_pool_pages, indptr, indices, batch, flags, opt, hp);
+    if (st != DH_OK) return st;
+    if (stats) fill_stats(hp, batch, stats);
+    static_assert(sizeof(dh_plan_item) == sizeof(dh::Item), "item layout");
+    static_assert(sizeof(dh::SeqSlot) == 2 * sizeof(uint32_t), "seqslot layout");
+    if (items) {
+        if (*n_items < hp.items.size()) return fail(DH_EINVAL, "items array too small");
+        memcpy(items, hp.items.data(), hp.items.size() * sizeof(dh::Item));
+    }
+    if (pages) {
+        if (*n_pages < hp.pages.size()) return fail(DH_EINVAL, "pages array too small");
+        memcpy(pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
+    }
+    if (seqslots) {
+        if (*n_seqslots < hp.seqslots.size()) return fail(DH_EINVAL, "seqslots array too small");
+        memcpy(seqslots, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
+    }
+    *n_items = uint32_t(hp.items.size());
+    *n_pages = uint32_t(hp.pages.size());
+    *n_seqslots = uint32_t(hp.seqslots.size());
+    return DH_OK;
+}
+
+dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                         const uint32_t* indptr, const uint32_t* indices, uint32_t batch,
+                         uint32_t flags, const dh_plan_options* opt, dh_plan** out) {
+    if (!be || !pool || !out || !cfg) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    if (pool->hkv != cfg->num_kv_heads || pool->d != cfg->head_dim || pool->fmt != cfg->kv_format)
+        return fail(DH_EINVAL, "pool (kv heads %u, head_dim %u, format %u) does not match the config "
+                    "(%u, %u, %u)", pool->hkv, pool->d, pool->fmt, cfg->num_kv_heads, cfg->head_dim,
+                    cfg->kv_format);
+    dh::HostPlan hp;
+    dh_status st = host_plan(cfg, pool->num_pages, indptr, indices, batch, flags, opt, hp);
+    if (st != DH_OK) return st;
 
     dh_plan* pl = new (std::nothrow) dh_plan;
     if (!pl) return fail(DH_ENOMEM, "out of host memory");
@@ -416,10 +525,12 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     memcpy(blob.data() + o_pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
     memcpy(blob.data() + o_ss, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
     memcpy(blob.data() + o_sp, hp.slot_ptr.data(), hp.slot_ptr.size() * sizeof(uint32_t));
-    hipError_t e = hipSetDevice(be->device);
+    dh::DeviceGuard guard(be->device);
+    hipError_t e = guard.error();
     if (e == hipSuccess) e = hipMalloc(&pl->dev, total);
     if (e == hipSuccess) e = hipMemcpy(pl->dev, blob.data(), total, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
+        (void)hipGetLastError();
         if (pl->dev) (void)hipFree(pl->dev);
         delete pl;
         return fail(DH_EHIP, "plan upload failed: %s", hipGetErrorString(e));
@@ -432,25 +543,21 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     const size_t rows = size_t(hp.num_slots) * cfg->num_heads;
     pl->ws_lse_off = align_up(rows * cfg->head_dim * sizeof(float), 256);
     pl->ws_bytes = align_up(pl->ws_lse_off + rows * sizeof(float), 256);
-    pl->stats.batch_size = batch;
-    pl->stats.num_segments = hp.num_segments;
-    pl->stats.num_shared_segments = hp.num_shared_segments;
-    pl->stats.num_items = pl->n_items;
-    pl->stats.num_tasks = pl->n_tasks;
-    pl->stats.num_group_items = hp.num_group_items;
-    pl->stats.num_partials = hp.num_slots;
-    pl->stats.unique_pages = hp.unique_pages;
-    pl->stats.page_reads = hp.page_reads;
-    pl->stats.total_pages = hp.total_pages;
+    fill_stats(hp, batch, &pl->stats);
+    retain(be);
     *out = pl;
     return DH_OK;
 }
 
 dh_status dh_plan_destroy(dh_plan* pl) {
     if (!pl) return DH_OK;
-    (void)hipSetDevice(pl->be->device);
-    (void)hipDeviceSynchronize();
-    (void)hipFree(pl->dev);
+    {
+        dh::DeviceGuard g(pl->be->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(pl->dev);
+        (void)hipGetLastError();
+    }
+    release(pl->be);
     delete pl;
     return DH_OK;
 }
@@ -481,7 +588,7 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         return fail(DH_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes the plan needs",
                     ws_bytes, pl->ws_bytes);
     if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
-    DH_HIP(hipSetDevice(be->device));
+    DH_DEVICE(be->device);
     const dh_attn_config& c = pl->cfg;
     float* ws_o = static_cast<float*>(ws);
     float* ws_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
@@ -552,7 +659,7 @@ dh_status dh_gather_debug(const dh_pool* pool, const uint32_t* ids, uint32_t n, 
     }
     *n_out = uint32_t(sel.size());
     if (sel.empty()) return DH_OK;
-    DH_HIP(hipSetDevice(pool->be->device));
+    DH_DEVICE(pool->be->device);
     uint32_t* d_ids = nullptr;
     DH_HIP(hipMalloc(&d_ids, sel.size() * sizeof(uint32_t)));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -571,7 +678,7 @@ dh_status dh_debug_e4m3_to_bf16(int device, const uint8_t* codes, const uint8_t*
     if (n % 4) return fail(DH_EINVAL, "n must be a multiple of 4");
     if (n == 0) return DH_OK;
     if (!codes || !e8m0 || !out) return fail(DH_EINVAL, "NULL argument");
-    DH_HIP(hipSetDevice(device));
+    DH_DEVICE(device);
     uint8_t* buf = nullptr;
     const size_t nb = size_t(n) + n / 4 + size_t(n) * 2;
     DH_HIP(hipMalloc(&buf, nb));

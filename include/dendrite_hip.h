@@ -106,8 +106,9 @@ typedef struct dh_attn_config {
     uint32_t num_kv_heads;    /* KV heads; num_heads % num_kv_heads == 0       */
     uint32_t head_dim;        /* 64, 128 or 256 (flashinfer/mod.rs:20)         */
     float scale;              /* softmax scale, 1/sqrt(head_dim) by default    */
-    uint32_t sliding_window;  /* 0 = None.  No Dendrite backend reads it; a
-                                 non-zero value returns DH_EUNSUPPORTED.       */
+    uint32_t sliding_window;  /* 0 = None.  Accepted and ignored, as by every
+                                 Dendrite backend (backend.rs:206-265 never
+                                 reads it): attention spans all tokens.       */
     uint32_t gqa_mapping;     /* dh_gqa_mapping, DH_GQA_TILED by default       */
     uint32_t q_dtype;         /* dh_dtype of q and out (out dtype = q dtype)   */
     uint32_t kv_format;       /* dh_kv_format of the pool this config reads    */
@@ -235,6 +236,27 @@ typedef struct dh_plan_stats {
     uint64_t total_pages;         /* pages over all sequences (naive reads)   */
 } dh_plan_stats;
 dh_status dh_plan_get_stats(const dh_plan* plan, dh_plan_stats* stats);
+
+/* One attention work item of a plan: pages[page_off .. +npages) of the plan's
+ * page list, KV head kv_head, query rows row_begin .. +nrows of its
+ * (segment, chunk).  Row rho belongs to sequence seqslots[seq_off + rho / r]
+ * (r = num_heads / num_kv_heads), query head offset rho % r. */
+typedef struct dh_plan_item {
+    uint32_t page_off, npages, seq_off, row_begin, nrows, kv_head, flags, tail_seq;
+} dh_plan_item;
+
+/* Host-only planning for tests and tools: runs the same planner as
+ * dh_plan_create on host inputs (no backend, no device) and copies out its
+ * tables.  Call with NULL arrays to learn the sizes (*n_items, *n_pages,
+ * *n_seqslots); seqslots receives (sequence, partial slot) pairs.  No
+ * counterpart in the reference (a test export like dh_gather_debug). */
+dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages,
+                          const uint32_t* indptr, const uint32_t* indices,
+                          uint32_t batch_size, uint32_t flags,
+                          const dh_plan_options* options, dh_plan_stats* stats,
+                          dh_plan_item* items, uint32_t* n_items,
+                          uint32_t* pages, uint32_t* n_pages,
+                          uint32_t* seqslots, uint32_t* n_seqslots);
 
 /* ------------------------------------------------------------------ decode */
 

@@ -1,0 +1,124 @@
+"""The C ABI without a GPU: libdendrite_hip.so loads, exports every function
+include/dendrite_hip.h declares, and its host-side entry points behave as
+documented (no device compute is called here)."""
+import ctypes as C
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from dendrite_amd import _lib
+from dendrite_amd.backend import AttentionConfig
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dendrite_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    names = set(re.findall(r"\b(dh_[a-z0-9_]+)\s*\(", text))
+    typedefs = set(re.findall(r"typedef\s+(?:struct|enum)?\s*\w*\s*\{?[^;]*?\b(dh_[a-z0-9_]+)\s*;", text))
+    return sorted(names - typedefs)
+
+
+def test_library_exports_every_declared_function():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) > 60
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # and the ctypes signature table covers them all
+    assert not [n for n in names if n not in _lib.SIGNATURES]
+
+
+def test_version_and_errors():
+    L = _lib.lib()
+    assert b"gfx950" in C.string_at(L.dh_version())
+    assert L.dh_attn_config_init(None, 8, 8, 64) == _lib.DH_EINVAL
+    assert b"NULL" in C.string_at(L.dh_last_error())
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_config_scale_is_f32_inverse_sqrt(d):
+    """backend.rs:37: scale = 1.0 / (head_dim as f32).sqrt(), in f32."""
+    c = AttentionConfig(32, 8, d)
+    assert c.scale == float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    assert c.num_queries_per_kv() == 4
+    assert _lib.lib().dh_attn_config_num_queries_per_kv(C.byref(c.to_c())) == 4
+    assert abs(c.scale - 1 / math.sqrt(d)) < 1e-7
+
+
+def test_default_config():
+    c = AttentionConfig.default()         # backend.rs:54-58
+    assert (c.num_heads, c.num_kv_heads, c.head_dim) == (8, 8, 64)
+    assert c.gqa_mapping == _lib.GQA_TILED
+
+
+def test_no_device_is_reported_not_crashed():
+    n = C.c_int(-1)
+    assert _lib.lib().dh_device_count(C.byref(n)) == _lib.DH_OK
+    if n.value > 0:
+        pytest.skip("a GPU is present")
+    h = C.c_void_p()
+    assert _lib.lib().dh_create(0, C.byref(h)) == _lib.DH_EUNSUPPORTED
+    assert not h.value
+    assert _lib.lib().dh_is_available() == 0
+
+
+def test_synth_normal_is_deterministic_and_normal():
+    L = _lib.lib()
+    a = np.array([L.dh_synth_normal(7, i) for i in range(20000)])
+    assert np.array_equal(a, [L.dh_synth_normal(7, i) for i in range(20000)])
+    assert abs(a.mean()) < 0.03 and abs(a.std() - 1) < 0.03
+    out = np.zeros(20000, dtype=np.uint16)
+    assert L.dh_synth_fill(out.ctypes.data, _lib.DTYPE_BF16, 7, 0, 20000) == 0
+    want = torch.from_numpy(a).float().to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("fmt", [_lib.KV_FP8_E4M3, _lib.KV_MXFP8])
+def test_synth_fp8_pages_round_like_torch(fmt):
+    """The synthetic page encoder rounds to nearest even and saturates at 448,
+    like torch's float8_e4m3fn conversion of the pre-clamped value."""
+    L = _lib.lib()
+    hkv, d = 2, 64
+    ids = np.array([3, 9], dtype=np.uint32)
+    page_elems = 2 * hkv * 16 * d
+    data = np.zeros((2, page_elems), dtype=np.uint8)
+    sbytes = 2 * hkv * 4 if fmt == _lib.KV_FP8_E4M3 else 2 * hkv * 16 * (d // 32)
+    scales = np.zeros((2, sbytes), dtype=np.uint8)
+    assert L.dh_synth_pages(fmt, hkv, d, 5, ids.ctypes.data_as(_lib._PU32), 2, C.c_double(20.0), 50, data.ctypes.data,
+                            scales.ctypes.data) == 0
+    for row, pid in enumerate(ids):
+        x = np.array([L.dh_synth_normal(5, int(pid) * page_elems + e) for e in range(page_elems)],
+                     dtype=np.float32)
+        x = x.reshape(2 * hkv, 16 * d)
+        codes = data[row].reshape(2 * hkv, 16 * d)
+        if fmt == _lib.KV_FP8_E4M3:
+            sc = scales[row].view(np.float32)
+            # outliers are placed by a hash; recover them from the codes' magnitudes
+            for blk in range(2 * hkv):
+                xs = torch.from_numpy(x[blk]).double()
+                dec = torch.from_numpy(codes[blk]).view(torch.float8_e4m3fn).double() * float(sc[blk])
+                ok = (dec.abs() < 19.0) & (xs.abs() < 19.0)
+                want = (xs / float(sc[blk])).clamp(-448, 448).float().to(torch.float8_e4m3fn)
+                got = torch.from_numpy(codes[blk]).view(torch.float8_e4m3fn)
+                assert torch.equal(got.view(torch.uint8)[ok], want.view(torch.uint8)[ok])
+        else:
+            e = scales[row].reshape(2 * hkv, 16 * d // 32).astype(np.float64) - 127
+            sc = np.repeat(np.ldexp(1.0, e.astype(np.int64)), 32, axis=1)
+            got = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn)
+            dec = got.double().numpy() * sc
+            ok = torch.from_numpy((np.abs(dec) < 19.0) & (np.abs(x) < 19.0))
+            # OCP MX: elements beyond the E4M3 range after scaling saturate
+            want = torch.from_numpy(x / sc).clamp(-448, 448).float().to(torch.float8_e4m3fn)
+            assert torch.equal(got.view(torch.uint8)[ok], want.view(torch.uint8)[ok])
+            # scale = 2^(floor(log2 amax) - 8) of each group of 32 (checked on
+            # groups without outliers)
+            amax = np.abs(x).reshape(2 * hkv, -1, 32).max(axis=2)
+            clean = ok.numpy().reshape(2 * hkv, -1, 32).all(axis=2)
+            assert np.array_equal(e[clean], (np.floor(np.log2(amax)) - 8)[clean])
