@@ -89,6 +89,18 @@ def cpu_baseline(w, budget_s: float = 12.0):
     }
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the attention kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy
+    calibration), or None when no summary for this workload exists."""
+    path = os.path.join(ROOT, "profiles", f"attend16_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get("hbm_bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,6 +112,9 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -108,6 +123,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return
 
     from dendrite_amd.backend import Backend, DecodePlan, Pool, decode_batch, raw_to_tensor
 
@@ -174,6 +199,7 @@ def main():
     log(f"[bench] step {ms_step * 1e3:.2f} us (attend {ms_attend * 1e3:.2f} us, merge {ms_merge * 1e3:.2f} us)"
         f"; single-step median {np.median(per) * 1e3:.2f} us")
 
+    traffic = measured_traffic(w0.name)
     gbs = alg / (ms_step * 1e-3) / 1e9
     attend_gbs = alg_attend / (ms_attend * 1e-3) / 1e9
     result = {
@@ -211,7 +237,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(attend_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "avg_launch_us": round(ms_attend * 1e3, 3),
             "merge_launch_us": round(ms_merge * 1e3, 3),
             "mfma_tflops": round(w0.flops() / (ms_attend * 1e-3) / 1e12, 2),
