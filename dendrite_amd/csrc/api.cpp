@@ -434,6 +434,8 @@ static dh_status host_plan(const dh_attn_config* cfg, uint32_t num_pool_pages, c
     in.hq = cfg->num_heads;
     in.hkv = cfg->num_kv_heads;
     in.wave_items_only = cfg->q_dtype == DH_DTYPE_F32;
+    in.group_rows = uint32_t(dh::group_rows(cfg->kv_format == DH_KV_FP8_E4M3 || cfg->kv_format == DH_KV_MXFP8,
+                                            int(cfg->head_dim)));
     in.cascade = (flags & DH_PLAN_CASCADE) != 0;
     if (opt) {
         in.shared_chunk_pages = opt->shared_chunk_pages;

@@ -133,6 +133,17 @@ __device__ __forceinline__ f4 mma16(const uint32_t* a, const uint32_t* b, f4 c) 
     }
 }
 
+// acc *= alpha in place.  The rescale runs on a rarely taken branch; done
+// through "+v" operands the accumulator keeps its registers on both paths,
+// so the compiler needs no copies of the accumulators to merge the paths.
+__device__ __forceinline__ void scale_inplace(f4& acc, float alpha) {
+    float x = acc[0], y = acc[1], z = acc[2], w = acc[3];
+    asm volatile("v_mul_f32 %0, %0, %4\n\tv_mul_f32 %1, %1, %4\n\tv_mul_f32 %2, %2, %4\n\tv_mul_f32 %3, %3, %4"
+                 : "+v"(x), "+v"(y), "+v"(z), "+v"(w)
+                 : "v"(alpha));
+    acc = f4{x, y, z, w};
+}
+
 // Query head served by row rho of an item (GQA mapping per dh_gqa_mapping).
 __device__ __forceinline__ void row_target(const AttendArgs& a, const Item& it, uint32_t row,
                                            uint32_t& seq, uint32_t& slot, uint32_t& qh) {
@@ -164,8 +175,9 @@ __device__ __forceinline__ int item_last_len(const AttendArgs& a, const Item& it
 // Writes the partial states of one wave's rows: tiles rt < nrt, row
 // row0 + 16*rt + c of the item.  O[rt][e][i] is element d = (4g+i)*EPL + e.
 // lrow[rt]: the row's total weight when ROW_SUMMED, else this lane's share
-// (summed over the row's four lanes here).
-template <int D, int RT, bool ROW_SUMMED>
+// (summed over the row's four lanes here).  TR: the accumulators come from
+// transposed V reads instead, O[rt][e][i] is element d = 16e + 4g + i.
+template <int D, int RT, bool ROW_SUMMED, bool TR = false>
 __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const Item& it, uint32_t row0,
                                                    int nrt, const float (&m)[RT], const float (&lrow)[RT],
                                                    const f4 (&O)[RT][D / 16], int g, int c) {
@@ -181,13 +193,18 @@ __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const It
             const uint32_t dst = slot * a.hq + qh;
             const float inv = lt > 0.f ? 1.f / lt : 0.f;
             float* o = a.ws_o + uint64_t(dst) * D;
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            if constexpr (TR) {
                 #pragma unroll
-                for (int e = 0; e < EPL; e += 4) {
-                    f4 v = {O[rt][e][i] * inv, O[rt][e + 1][i] * inv, O[rt][e + 2][i] * inv,
-                            O[rt][e + 3][i] * inv};
-                    *reinterpret_cast<f4*>(o + (4 * g + i) * EPL + e) = v;
+                for (int e = 0; e < EPL; ++e) *reinterpret_cast<f4*>(o + 16 * e + 4 * g) = O[rt][e] * inv;
+            } else {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e += 4) {
+                        f4 v = {O[rt][e][i] * inv, O[rt][e + 1][i] * inv, O[rt][e + 2][i] * inv,
+                                O[rt][e + 3][i] * inv};
+                        *reinterpret_cast<f4*>(o + (4 * g + i) * EPL + e) = v;
+                    }
                 }
             }
             if (g == 0) a.ws_lse[dst] = lt > 0.f ? m[rt] + log2f(lt) : kNegInf;
@@ -250,14 +267,13 @@ __device__ __forceinline__ void pair_scores(const uint32_t (&kop)[2][D / 32][4],
 // the weights the PV MFMAs used (O / L is then a convex combination of V rows
 // whatever the rounding of P).
 template <int D, bool F16, int NRT, int RT, bool BLOCK_SCALE>
-__device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint32_t (&vop)[2][4][D / 32],
-                                                int n0, int n1, float f0, float f1, float v0s, float v1s,
-                                                float (&m)[RT], f4 (&L)[RT], f4 (&O)[RT][D / 16], int g) {
+__device__ __forceinline__ void pair_softmax(const f4 (&s)[RT][2], int n0, int n1, float f0, float f1,
+                                             float v0s, float v1s, float (&m)[RT], f4 (&L)[RT],
+                                             f4 (&O)[RT][D / 16], int g, uint32_t (&pB)[RT][4]) {
     constexpr int EPL = D / 16;
     constexpr float kLazy = 8.f;                  // running-max slack (log2 units)
     const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
     const uint32_t ones[4] = {one2, one2, one2, one2};
-    uint32_t pB[RT][4];
     const bool full = (n0 == kPageSize) && (n1 == kPageSize);
     #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
@@ -283,9 +299,9 @@ __device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint
             const float mnew = mx > m[rt] + kLazy ? mx : m[rt];
             const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
             m[rt] = mnew;
-            L[rt] *= alpha;
+            scale_inplace(L[rt], alpha);
             #pragma unroll
-            for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
+            for (int e = 0; e < EPL; ++e) scale_inplace(O[rt][e], alpha);
         }
         const float nm = (m[rt] == kNegInf) ? 0.f : -m[rt];
         #pragma unroll
@@ -309,6 +325,15 @@ __device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint
             for (int k = 0; k < 4; ++k) pB[rt][k] = pk[k];
         }
     }
+}
+
+template <int D, bool F16, int NRT, int RT, bool BLOCK_SCALE>
+__device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint32_t (&vop)[2][4][D / 32],
+                                                int n0, int n1, float f0, float f1, float v0s, float v1s,
+                                                float (&m)[RT], f4 (&L)[RT], f4 (&O)[RT][D / 16], int g) {
+    constexpr int EPL = D / 16;
+    uint32_t pB[RT][4];
+    pair_softmax<D, F16, NRT, RT, BLOCK_SCALE>(s, n0, n1, f0, f1, v0s, v1s, m, L, O, g, pB);
     // The V operand of a d-block (element e of the lane's 8 tokens) is
     // shared by all row tiles.
     #pragma unroll
@@ -682,9 +707,11 @@ __device__ __forceinline__ void group_loop(const AttendArgs& a, const Item& it, 
 }
 
 template <int D, uint32_t KVF, bool F16>
-__device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, uint8_t* lds, int tid,
-                                           int wave, int g, int c) {
-    constexpr int RT = kGroupTiles;
+__device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, int tid, int wave, int g,
+                                           int c) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * GroupLayout<D, KVF>::STAGE +
+                                                        kGroupMaxPages * 4 * (KVF == KVF_FP8 ? 3 : 1)];
+    constexpr int RT = kGroupTiles8;
     constexpr int EPL = D / 16;
     constexpr int KB = D / 32;
     // The item's page ids (and FP8 block scales) go to LDS once, so the pair
@@ -725,12 +752,418 @@ __device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, 
     write_wave_partial<D, RT, true>(a, it, row0, nrt, m, lr, O, g, c);
 }
 
+// ------------------------------------------------- group items, 16-bit KV
+// Pages reach LDS by direct global->LDS loads (global_load_lds_dwordx4, one
+// 1 KiB wave load per 64 lanes x 16 bytes): no staging registers and no
+// VALU work.  The ring is two LDS objects ("halves") of H page pairs each:
+// while the waves compute the H pairs of one half, the loads of the next H
+// pairs fill the other.  Because the halves are distinct objects the
+// compiler tracks which loads each read depends on and waits exactly; the
+// explicit waits before each barrier make every wave's loads visible to all.
+//
+// A slot holds one page: the K plane (16 rows) then the V plane.  The
+// 16-byte chunks of row r are XOR-swizzled (chunk j at position j ^ swz(r)),
+// which keeps both read patterns free of bank conflicts:
+//   K (A operand of the scores): lane (g, c) reads row c, chunk 4kb + g;
+//   V (A operand of O^T, by ds_read_b64_tr_b16): lane (g, c) reads 8 bytes of
+//   row 4g + c/4 at dims 16e + 4(c%4); within each 16-lane group the
+//   transpose hands lane c the values V[4g + j][16e + c], j = 0..3 — the
+//   MFMA's k = 4g + j slots — so the accumulators hold O[row][16e + 4g + i].
+// Each wave owns row tiles w, w+4, w+8, w+12 of the item (up to 256 rows).
+template <int D>
+struct DmaCfg {
+    static constexpr int RB = 2 * D;                  // bytes per row
+    static constexpr int PLANE = kPageSize * RB;
+    static constexpr int PAGE = 2 * PLANE;            // 4, 8 or 16 KiB
+    static constexpr int RING = D == 256 ? 128 * 1024 : 64 * 1024;   // LDS bytes of the ring
+    static constexpr int NP = RING / (2 * PAGE);      // page pairs in the ring
+    static constexpr int DPP = PAGE / (kWaves * 64 * 16);   // wave loads per thread per page
+    static constexpr int PER_PAIR = 2 * DPP;          // loads per thread per pair
+    static constexpr int RT = group_tiles16(D);       // row tiles per wave
+    static_assert(DPP >= 1 && PLANE % 1024 == 0, "a page must split into 1 KiB wave loads");
+    static_assert(NP >= 3 && (NP - 2) * PER_PAIR <= 48, "vmcnt cases");
+    static_assert(DPP <= 4, "DmaSrc holds four offsets");
+};
+
+template <int D>
+__device__ __forceinline__ int chunk_swz(int row) {
+    if constexpr (D == 64) return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+    else return ((row & 7) << 1) | (row >> 3);
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <bool F16>
+__device__ __forceinline__ f4 mma16v(u32x4 a, u32x4 b, f4 c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                      c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// s_waitcnt vmcnt(n) for even n <= 48 (s_waitcnt takes an immediate).
+__device__ __forceinline__ void wait_vmcnt(uint32_t n) {
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+        case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+        case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+        case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+        case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+        case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+        case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+        case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+        case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+        case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+        case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+        case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+        case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+        case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+        case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
+        case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
+        case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
+        case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
+        case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
+        case 44: asm volatile("s_waitcnt vmcnt(44)" ::: "memory"); break;
+        case 46: asm volatile("s_waitcnt vmcnt(46)" ::: "memory"); break;
+        case 48: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
+// Barrier after this wave's LDS reads have returned (lgkmcnt(0)), so no
+// read of a slot can still be in flight when another wave refills it.
+__device__ __forceinline__ void block_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+}
+
+// Lane byte offsets inside a slot of the K operand reads (per k-block) and
+// the transposed V reads (per d-block).
+template <int D>
+struct LdsOffsets {
+    uint32_t k[D / 32];
+    uint32_t v[D / 16];
+};
+
+template <int D>
+__device__ __forceinline__ LdsOffsets<D> lds_offsets(int g, int c) {
+    using C = DmaCfg<D>;
+    LdsOffsets<D> o;
+    #pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) o.k[kb] = c * C::RB + (((4 * kb + g) ^ chunk_swz<D>(c)) << 4);
+    const int row = 4 * g + (c >> 2);
+    #pragma unroll
+    for (int e = 0; e < D / 16; ++e)
+        o.v[e] = C::PLANE + row * C::RB + (((2 * e + ((c & 3) >> 1)) ^ chunk_swz<D>(row)) << 4) + ((c & 1) << 3);
+    return o;
+}
+
+// Zeroes the V values of tokens 4g + j >= n (j = 0..3) in one page's half
+// (dwords w0, w0+1) of a transposed V operand.
+__device__ __forceinline__ void mask_v_tr(u32x4& v, int w0, int g, int n) {
+    #pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const int t = 4 * g + 2 * w;
+        const uint32_t keep = (t < n ? 0x0000FFFFu : 0u) | (t + 1 < n ? 0xFFFF0000u : 0u);
+        v[w0 + w] &= keep;
+    }
+}
+
+// Online softmax of a pair's scores (see pair_softmax), vector operands.
+// PARTIAL: some token of the pair may be invalid.
+template <bool F16, int NRT, int RT, int EPL, bool PARTIAL>
+__device__ __forceinline__ void dma_softmax(const f4 (&s)[RT][2], int n0, int n1, float f, float (&m)[RT],
+                                            f4 (&L)[RT], f4 (&O)[RT][EPL], int g, u32x4 (&pB)[RT]) {
+    constexpr float kLazy = 8.f;
+    const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
+    const u32x4 ones = {one2, one2, one2, one2};
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        f4 x0 = s[rt][0], x1 = s[rt][1];
+        if constexpr (PARTIAL) {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (4 * g + i >= n0) x0[i] = kNegInf;
+                if (4 * g + i >= n1) x1[i] = kNegInf;
+            }
+        }
+        const float lm = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
+                               fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]))) * f;
+        // The reference max moves only when a score passes it by kLazy; the
+        // accumulators are then rescaled.  The rescale is unconditional
+        // (alpha = 1 otherwise): a branch around it costs more in register
+        // copies than the multiplies do.
+        float mnew = m[rt];
+        if (__ballot(lm > m[rt] + kLazy)) {
+            const float mx = rowgroup_max(lm);
+            mnew = mx > m[rt] + kLazy ? mx : m[rt];
+        }
+        const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+        m[rt] = mnew;
+        L[rt] *= alpha;
+        #pragma unroll
+        for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
+        const float nm = (mnew == kNegInf) ? 0.f : -mnew;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x0[i] = fast_exp2(__builtin_fmaf(x0[i], f, nm));
+            x1[i] = fast_exp2(__builtin_fmaf(x1[i], f, nm));
+        }
+        pB[rt] = u32x4{pack2(x0[0], x0[1], F16), pack2(x0[2], x0[3], F16), pack2(x1[0], x1[1], F16),
+                       pack2(x1[2], x1[3], F16)};
+        L[rt] = mma16v<F16>(ones, pB[rt], L[rt]);
+    }
+}
+
+struct DmaSrc {
+    uint32_t loff[4];                 // this lane's source offsets inside a page (DPP <= 4)
+    uint64_t page_stride;
+};
+
+// One wave load of 64 x 16 bytes from gbase + voff (per lane) to the LDS
+// address lds (wave-uniform) + 16 * lane.  Issued from inline assembly: the
+// compiler does not track it, so it adds no drain of its own before the LDS
+// reads; the pair loop waits for it with explicit vmcnt counts.
+__device__ __forceinline__ void dma_x4(uint32_t lds, const void* gbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory", "m0");
+}
+
+// Issues this wave's share of the loads of pair `pair` into pair slot `ps`.
+template <int D>
+__device__ __forceinline__ void dma_pair(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                         const DmaSrc& src, uint32_t ring, uint32_t pair, uint32_t ps, int wave) {
+    using C = DmaCfg<D>;
+    const uint32_t np = it.npages;
+    #pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t i = 2 * pair + q < np ? 2 * pair + q : np - 1;
+        const uint32_t pg = __builtin_amdgcn_readfirstlane(ids[i]);
+        const uint8_t* base = a.kv + uint64_t(pg) * src.page_stride;
+        const uint32_t slot = ring + (2 * ps + q) * C::PAGE + wave * C::DPP * 1024;
+        #pragma unroll
+        for (int u = 0; u < C::DPP; ++u) dma_x4(slot + u * 1024, base, src.loff[u]);
+    }
+}
+
+// The math of one page pair (slots s0 and s0 + PAGE of the ring).
+template <int D, bool F16, int NRT, bool TAIL>
+__device__ __forceinline__ void dma_pair_math(const AttendArgs& a, const uint8_t* s0, const LdsOffsets<D>& lo,
+                                              int n0, int n1, int g, const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                              float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
+                                              f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+    using C = DmaCfg<D>;
+    constexpr int RT = C::RT, KB = D / 32, EPL = D / 16;
+    const uint8_t* s1 = s0 + C::PAGE;
+    f4 sc[RT][2];
+    {
+        u32x4 kop[2][KB];
+        #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            kop[0][kb] = *reinterpret_cast<const u32x4*>(s0 + lo.k[kb]);
+            kop[1][kb] = *reinterpret_cast<const u32x4*>(s1 + lo.k[kb]);
+        }
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            sc[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
+            sc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                sc[rt][0] = mma16v<F16>(kop[0][kb], qB[rt][kb], sc[rt][0]);
+                sc[rt][1] = mma16v<F16>(kop[1][kb], qB[rt][kb], sc[rt][1]);
+            }
+        }
+    }
+    u32x4 pB[RT];
+    const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
+    if (partial)
+        dma_softmax<F16, NRT, RT, EPL, true>(sc, n0, n1, a.scale_log2, m, Lsum, O, g, pB);
+    else
+        dma_softmax<F16, NRT, RT, EPL, false>(sc, n0, n1, a.scale_log2, m, Lsum, O, g, pB);
+    #pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s0 + lo.v[e]));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s1 + lo.v[e]));
+        u32x4 vA = __builtin_shufflevector(__builtin_bit_cast(u32x2, v0), __builtin_bit_cast(u32x2, v1), 0, 1, 2,
+                                           3);
+        if constexpr (TAIL) {
+            if (partial) {
+                mask_v_tr(vA, 0, g, n0);
+                mask_v_tr(vA, 2, g, n1);
+            }
+        }
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vA, pB[rt], O[rt][e]);
+    }
+}
+
+template <int D, bool F16, int NRT, bool TAIL>
+__device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                               uint8_t* ring, int tid, int wave, int g, int c,
+                                               const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                               float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
+                                               f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+    using C = DmaCfg<D>;
+    constexpr uint32_t P = C::NP;
+    const int last_len = TAIL ? item_last_len(a, it) : kPageSize;
+    const uint32_t np = it.npages;
+    const uint32_t npairs = (np + 1) >> 1;
+    DmaSrc src;
+    src.page_stride = uint64_t(2) * a.hkv * C::PLANE;
+    #pragma unroll
+    for (int u = 0; u < C::DPP; ++u) {
+        const int b = (wave * C::DPP + u) * 1024 + 16 * (tid & 63);
+        const int plane = b / C::PLANE, rem = b - plane * C::PLANE;
+        const int row = rem / C::RB, pos = (rem - row * C::RB) >> 4;
+        const int j = pos ^ chunk_swz<D>(row);
+        src.loff[u] = uint32_t((plane * a.hkv + it.kv_head) * C::PLANE + row * C::RB + j * 16);
+    }
+    const LdsOffsets<D> lo = lds_offsets<D>(g, c);
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
+    // Every load the compiler issued (the query rows, the last page length)
+    // lands before the ring loads start, so the loop holds no compiler-tracked
+    // load and no compiler-inserted wait can drain the ring.
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    compiler_fence();
+    const uint32_t pro = min(P - 1, npairs);
+    #pragma unroll 1
+    for (uint32_t q = 0; q < pro; ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
+    uint32_t ps = 0;
+    #pragma unroll 1
+    for (uint32_t pi = 0; pi < npairs; ++pi) {
+        // Issued so far: pairs < min(pi + P - 1, npairs); pair pi must have landed.
+        wait_vmcnt((min(pi + P - 1, npairs) - pi - 1) * C::PER_PAIR);
+        block_barrier();
+        if (pi + P - 1 < npairs)
+            dma_pair<D>(a, it, ids, src, ring_lds, pi + P - 1, ps == 0 ? P - 1 : ps - 1, wave);
+        const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
+        const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
+        if constexpr (NRT > 0)
+            dma_pair_math<D, F16, NRT, TAIL>(a, ring + ps * 2 * C::PAGE, lo, n0, n1, g, qB, m, Lsum, O);
+        ps = ps + 1 == P ? 0 : ps + 1;
+    }
+    // The last pair's wait was vmcnt(0): no ring load is outstanding.
+}
+
+// Query rows of a wave's tiles in a DMA group item: tile rt of wave w covers
+// rows (rt * kWaves + w) * 16 .. +16.
+template <int D, int RT>
+__device__ __forceinline__ void load_q_dma(const AttendArgs& a, const Item& it, int wave, int g, int c,
+                                           u32x4 (&qB)[RT][D / 32]) {
+    constexpr int KB = D / 32;
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
+        if (row < it.nrows) {
+            uint32_t seq, slot, qh;
+            row_target(a, it, row, seq, slot, qh);
+            const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) qB[rt][kb] = *reinterpret_cast<const u32x4*>(qp + kb * 32 + 8 * g);
+        } else {
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) qB[rt][kb] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+template <int D, int RT>
+__device__ __forceinline__ void write_partial_dma(const AttendArgs& a, const Item& it, int wave, int nrt,
+                                                  const float (&m)[RT], const f4 (&L)[RT],
+                                                  const f4 (&O)[RT][D / 16], int g, int c) {
+    constexpr int EPL = D / 16;
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        if (rt >= nrt) break;
+        const uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
+        if (row < it.nrows) {
+            uint32_t seq, slot, qh;
+            row_target(a, it, row, seq, slot, qh);
+            const uint32_t dst = slot * a.hq + qh;
+            const float lt = L[rt][0];
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            float* o = a.ws_o + uint64_t(dst) * D;
+            #pragma unroll
+            for (int e = 0; e < EPL; ++e) *reinterpret_cast<f4*>(o + 16 * e + 4 * g) = O[rt][e] * inv;
+            if (g == 0) a.ws_lse[dst] = lt > 0.f ? m[rt] + log2f(lt) : kNegInf;
+        }
+    }
+}
+
+template <int D, bool F16, int NRT>
+__device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                              uint8_t* ring, int tid, int wave, int g, int c) {
+    using C = DmaCfg<D>;
+    constexpr int RT = C::RT, EPL = D / 16, KB = D / 32;
+    u32x4 qB[RT][KB];
+    load_q_dma<D, RT>(a, it, wave, g, c, qB);
+    float m[RT];
+    f4 L[RT];
+    f4 O[RT][EPL];
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = kNegInf;
+        L[rt] = f4{0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (it.flags & kItemTail)
+        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, qB, m, L, O);
+    else
+        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, qB, m, L, O);
+    write_partial_dma<D, RT>(a, it, wave, NRT, m, L, O, g, c);
+}
+
+// Item fields as wave-uniform values (they are: the item is the workgroup's),
+// so loop bounds and page addressing stay in scalar registers.
+__device__ __forceinline__ Item uniform_item(const Item& it) {
+    Item u;
+    u.page_off = __builtin_amdgcn_readfirstlane(it.page_off);
+    u.npages = __builtin_amdgcn_readfirstlane(it.npages);
+    u.seq_off = __builtin_amdgcn_readfirstlane(it.seq_off);
+    u.row_begin = __builtin_amdgcn_readfirstlane(it.row_begin);
+    u.nrows = __builtin_amdgcn_readfirstlane(it.nrows);
+    u.kv_head = __builtin_amdgcn_readfirstlane(it.kv_head);
+    u.flags = __builtin_amdgcn_readfirstlane(it.flags);
+    u.tail_seq = __builtin_amdgcn_readfirstlane(it.tail_seq);
+    return u;
+}
+
+template <int D, bool F16>
+__device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& item, int tid, int wave, int g,
+                                               int c) {
+    using C = DmaCfg<D>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[C::RING];
+    __shared__ uint32_t ids[kGroupMaxPages];
+    const Item it = uniform_item(item);
+    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) ids[i] = a.pages[it.page_off + i];
+    __syncthreads();
+    // Tiles of this wave that hold rows: tiles w, w+4, ... below ceil(nrows/16).
+    const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
+    const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
+    if (nrt >= 3) dma_group_run<D, F16, C::RT>(a, it, ids, ring, tid, wave, g, c);
+    else if (nrt == 2) dma_group_run<D, F16, 2>(a, it, ids, ring, tid, wave, g, c);
+    else if (nrt == 1) dma_group_run<D, F16, 1>(a, it, ids, ring, tid, wave, g, c);
+    else dma_group_run<D, F16, 0>(a, it, ids, ring, tid, wave, g, c);
+}
+
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
 template <int D, uint32_t KVF, bool F16>
 __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * GroupLayout<D, KVF>::STAGE +
-                                                        kGroupMaxPages * 4 * (KVF == KVF_FP8 ? 3 : 1)];
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     // Wave index as a wave-uniform (scalar) value: page-list reads then go
     // through the scalar cache and never wait on the vector loads in flight.
@@ -738,7 +1171,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     const Task t = a.tasks[blockIdx.x];
     if (t.kind == kTaskGroup) {
         const Item it = a.items[t.first];
-        group_item<D, KVF, F16>(a, it, lds, tid, wave, g, c);
+        if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
+        else group_item_dma<D, F16>(a, it, tid, wave, g, c);
     } else if (uint32_t(wave) < t.count) {
         const Item it = a.items[t.first + wave];
         wave_item<D, KVF, F16>(a, it, g, c);
@@ -832,31 +1266,65 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
 // ------------------------------------------------------------------ merge
 // One wave per (sequence, query head): log-sum-exp over the sequence's
 // partial states; no partial state -> zeros (backend.rs:218-222).
+// Lane l reads the log-sum-exp of slots l, l+64, ...; the wave reduces their
+// max and weights with cross-lane operations, then accumulates the slots'
+// O rows sixteen at a time so sixteen loads are in flight per lane instead of
+// one dependent load per slot.
+__device__ __forceinline__ float wave_max(float x) {
+    #pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+    #pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
 template <int D, uint32_t OUT>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     constexpr int PL = D / 64;
+    constexpr int U = 16;
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.batch * a.hq) return;
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
-    const uint32_t s0 = a.slot_ptr[b], s1 = a.slot_ptr[b + 1];
+    const uint32_t s0 = a.slot_ptr[b], n = a.slot_ptr[b + 1] - s0;
     float M = kNegInf;
-    for (uint32_t s = s0; s < s1; ++s) M = fmaxf(M, a.ws_lse[uint64_t(s) * a.hq + qh]);
+    for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh]);
+    M = wave_max(M);
     float acc[PL];
     #pragma unroll
     for (int k = 0; k < PL; ++k) acc[k] = 0.f;
     float W = 0.f;
     if (M != kNegInf) {
-        for (uint32_t s = s0; s < s1; ++s) {
-            const float L = a.ws_lse[uint64_t(s) * a.hq + qh];
-            if (L == kNegInf) continue;
-            const float w = fast_exp2(L - M);
-            W += w;
-            const float* o = a.ws_o + (uint64_t(s) * a.hq + qh) * D + lane * PL;
-            #pragma unroll
-            for (int k = 0; k < PL; ++k) acc[k] += w * o[k];
+        for (uint32_t base = 0; base < n; base += 64) {
+            // Weight of slot base + lane, then the slots' O rows in groups of U.
+            const uint32_t k = base + lane;
+            const float Lk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : kNegInf;
+            const float wk = Lk == kNegInf ? 0.f : fast_exp2(Lk - M);
+            W += wk;
+            const uint32_t cnt = min(64u, n - base);
+            for (uint32_t j0 = 0; j0 < cnt; j0 += U) {
+                float v[U][PL];
+                #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t j = min(j0 + u, cnt - 1);
+                    const float* o = a.ws_o + (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL;
+                    #pragma unroll
+                    for (int q = 0; q < PL; ++q) v[u][q] = o[q];
+                }
+                #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const float w = (j0 + u < cnt) ? __shfl(wk, int(j0 + u), 64) : 0.f;
+                    #pragma unroll
+                    for (int q = 0; q < PL; ++q) acc[q] += w * v[u][q];
+                }
+            }
         }
     }
+    W = wave_sum(W);
     const float inv = W > 0.f ? 1.f / W : 0.f;
     const uint64_t ob = (uint64_t(b) * a.hq + qh) * D + lane * PL;
     #pragma unroll

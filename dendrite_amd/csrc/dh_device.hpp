@@ -24,9 +24,16 @@ constexpr int kPageSize = 16;       // tokens per page (dendrite-ffi flashinfer/
 constexpr int kWaves = 4;           // wave64s per workgroup
 constexpr int kTileRows = 16;       // query rows of one MFMA tile
 constexpr int kWaveRows = 16;       // rows of a wave item: one tile, one wave
-constexpr int kGroupTiles = 1;      // tiles per wave in a group item
-constexpr int kGroupRows = kWaves * kGroupTiles * kTileRows;   // 64
 constexpr int kGroupMaxPages = 256; // pages of one group item (LDS page-id list)
+// Row tiles per wave of a group item: 16-bit KV pages (staged by direct
+// global->LDS loads) use two (one at head_dim 256, for registers), FP8 /
+// MXFP8 pages (staged through registers) one.  A group item has
+// kWaves * tiles * 16 rows.
+constexpr int kGroupTiles8 = 1;
+DH_HOST_DEVICE constexpr int group_tiles16(int head_dim) { return head_dim == 256 ? 1 : 2; }
+DH_HOST_DEVICE constexpr int group_rows(bool fp8_kv, int head_dim) {
+    return kWaves * (fp8_kv ? kGroupTiles8 : group_tiles16(head_dim)) * kTileRows;
+}
 
 // One attention work item (32 bytes): a run of pages of one segment chunk,
 // one KV head and a block of query rows.
@@ -43,8 +50,8 @@ struct Item {
 constexpr uint32_t kItemTail = 1u;
 
 // What one workgroup does: up to four wave items (one per wave, <= 16 rows
-// each) or one group item (<= 128 rows: each wave owns 32 rows and all four
-// waves read the same pages, staged once in LDS).
+// each) or one group item (<= group_rows() rows: each wave owns a block of
+// rows and all four waves read the same pages, staged once in LDS).
 struct Task {
     uint32_t kind;       // kTaskWaves or kTaskGroup
     uint32_t first;      // first item

@@ -154,22 +154,22 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
 
     // 3. Item classes and chunk sizes.  A segment with at most kWaveRows
     //    query rows becomes wave items (one wave each); a larger one becomes
-    //    group items of up to kGroupRows rows whose four waves share every
+    //    group items of up to in.group_rows rows whose four waves share every
     //    page through LDS.  Chunks split a segment's pages over items: more
     //    chunks give more parallelism and more partial states.
     auto is_group = [&](const Segment& sg) {
         return !in.wave_items_only && uint32_t(sg.seqs.size()) * r > uint32_t(kWaveRows);
     };
-    uint32_t group_chunk = std::min<uint32_t>(in.shared_chunk_pages ? in.shared_chunk_pages : 64,
+    uint32_t group_chunk = std::min<uint32_t>(in.shared_chunk_pages ? in.shared_chunk_pages : 32,
                                               kGroupMaxPages);
-    uint32_t wave_chunk = in.private_chunk_pages ? in.private_chunk_pages : 32;
+    uint32_t wave_chunk = in.private_chunk_pages ? in.private_chunk_pages : 8;
     const uint32_t target = in.target_items ? in.target_items : 1536;   // waves
     auto count_waves = [&](uint32_t gc, uint32_t wc) {
         uint64_t n = 0;
         for (const auto& sg : segs) {
             const uint32_t rows = uint32_t(sg.seqs.size()) * r;
             if (is_group(sg)) {
-                n += uint64_t(ceil_div(uint32_t(sg.pages.size()), gc)) * ceil_div(rows, kGroupRows) *
+                n += uint64_t(ceil_div(uint32_t(sg.pages.size()), gc)) * ceil_div(rows, in.group_rows) *
                      in.hkv * kWaves;
             } else {
                 n += uint64_t(ceil_div(uint32_t(sg.pages.size()), wc)) * ceil_div(rows, kWaveRows) * in.hkv;
@@ -213,7 +213,7 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         out.page_reads += np;
         const uint32_t nc = nchunks[s];
         const uint32_t rows = uint32_t(sg.seqs.size()) * r;
-        const uint32_t block = grp ? uint32_t(kGroupRows) : uint32_t(kWaveRows);
+        const uint32_t block = grp ? in.group_rows : uint32_t(kWaveRows);
         const uint32_t nrb = ceil_div(rows, block);
         for (uint32_t ci = 0; ci < nc; ++ci) {
             const uint32_t p0 = uint32_t(uint64_t(ci) * np / nc);

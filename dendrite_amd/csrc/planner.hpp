@@ -14,6 +14,7 @@ struct PlanInput {
     uint32_t num_pool_pages = 0;
     uint32_t hq = 0, hkv = 0;
     bool wave_items_only = false;       // f32: every item is a <= 16-row wave item
+    uint32_t group_rows = 128;          // rows of a group item (group_rows())
     bool cascade = true;
     uint32_t shared_chunk_pages = 0;    // 0 = default
     uint32_t private_chunk_pages = 0;
