@@ -103,13 +103,17 @@ class Backend:
 
     def __init__(self, device: int = 0):
         self._h = C.c_void_p()
+        self._destroy = lib().dh_destroy
         check(lib().dh_create(device, C.byref(self._h)))
         self.device = device
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_destroy(self._h)
-            self._h = C.c_void_p()
+        # Bound at construction: module globals may already be gone when an
+        # object is collected at interpreter shutdown.
+        destroy = getattr(self, "_destroy", None)
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def synchronize(self) -> None:
         check(lib().dh_synchronize(self._h))
@@ -131,6 +135,7 @@ class Pool:
                  kv_format: int = _lib.KV_BF16, page_size: int = _lib.PAGE_SIZE):
         self.backend = backend
         self._h = C.c_void_p()
+        self._destroy = lib().dh_pool_destroy
         check(lib().dh_pool_create(backend._h, num_pages, num_kv_heads, head_dim, page_size,
                                    kv_format, C.byref(self._h)))
         self.num_pages = num_pages
@@ -141,9 +146,12 @@ class Pool:
         self.scale_bytes = lib().dh_pool_scale_bytes(self._h)
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_pool_destroy(self._h)
-            self._h = C.c_void_p()
+        # Bound at construction: module globals may already be gone when an
+        # object is collected at interpreter shutdown.
+        destroy = getattr(self, "_destroy", None)
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def write_pages(self, page_ids, data: np.ndarray, scales: Optional[np.ndarray] = None,
                     stream=None) -> None:
@@ -218,6 +226,7 @@ class DecodePlan:
         opt.target_items = target_items
         self._c = config.to_c()
         self._h = C.c_void_p()
+        self._destroy = lib().dh_plan_destroy
         check(lib().dh_plan_create(backend._h, C.byref(self._c), pool._h,
                                    ip.ctypes.data_as(_lib._PU32),
                                    ix.ctypes.data_as(_lib._PU32) if len(ix) else None,
@@ -227,9 +236,12 @@ class DecodePlan:
         self.workspace_size = lib().dh_plan_workspace_size(self._h)
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_plan_destroy(self._h)
-            self._h = C.c_void_p()
+        # Bound at construction: module globals may already be gone when an
+        # object is collected at interpreter shutdown.
+        destroy = getattr(self, "_destroy", None)
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def stats(self) -> dict:
         s = _lib.dh_plan_stats()

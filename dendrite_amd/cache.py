@@ -54,6 +54,7 @@ class BlockTable:
 
     def __init__(self, tokens_per_block: int = 16, _handle=None):
         self._h = C.c_void_p()
+        self._destroy = lib().dh_block_table_destroy
         if _handle is not None:
             self._h = _handle
         else:
@@ -69,9 +70,10 @@ class BlockTable:
         return cls(tokens_per_block)
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_block_table_destroy(self._h)
-            self._h = C.c_void_p()
+        destroy = getattr(self, "_destroy", None)  # bound at construction
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def num_blocks(self) -> int:
         return lib().dh_block_table_num_blocks(self._h)
@@ -133,13 +135,15 @@ class BlockPool:
 
     def __init__(self, max_blocks: int, tokens_per_block: int = 16):
         self._h = C.c_void_p()
+        self._destroy = lib().dh_block_pool_destroy
         check(lib().dh_block_pool_create(max_blocks, tokens_per_block, C.byref(self._h)))
         self.tokens_per_block = tokens_per_block
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_block_pool_destroy(self._h)
-            self._h = C.c_void_p()
+        destroy = getattr(self, "_destroy", None)  # bound at construction
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def allocate(self) -> BlockId:
         out = C.c_uint32()
@@ -234,12 +238,14 @@ class TreeState:
     def __init__(self, kv_cache: KvCache, tokens_per_block: int = 16):
         self.kv_cache = kv_cache          # keeps the pool alive
         self._h = C.c_void_p()
+        self._destroy = lib().dh_tree_destroy
         check(lib().dh_tree_create(kv_cache.pool._h, tokens_per_block, C.byref(self._h)))
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().dh_tree_destroy(self._h)
-            self._h = C.c_void_p()
+        destroy = getattr(self, "_destroy", None)  # bound at construction
+        if destroy is not None and getattr(self, "_h", None) and self._h.value:
+            destroy(self._h)
+            self._h = None
 
     def fork(self, from_node: int) -> ForkHandle:
         child, depth, ntok = C.c_uint64(), C.c_uint64(), C.c_uint64()

@@ -880,50 +880,47 @@ __device__ __forceinline__ void mask_v_tr(u32x4& v, int w0, int g, int n) {
     }
 }
 
-// Online softmax of a pair's scores (see pair_softmax), vector operands.
-// PARTIAL: some token of the pair may be invalid.
-template <bool F16, int NRT, int RT, int EPL, bool PARTIAL>
-__device__ __forceinline__ void dma_softmax(const f4 (&s)[RT][2], int n0, int n1, float f, float (&m)[RT],
-                                            f4 (&L)[RT], f4 (&O)[RT][EPL], int g, u32x4 (&pB)[RT]) {
-    constexpr float kLazy = 8.f;
-    const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
-    const u32x4 ones = {one2, one2, one2, one2};
-    #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-        f4 x0 = s[rt][0], x1 = s[rt][1];
-        if constexpr (PARTIAL) {
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (4 * g + i >= n0) x0[i] = kNegInf;
-                if (4 * g + i >= n1) x1[i] = kNegInf;
-            }
-        }
-        const float lm = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
-                               fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]))) * f;
-        // The reference max moves only when a score passes it by kLazy; the
-        // accumulators are then rescaled.  The rescale is unconditional
-        // (alpha = 1 otherwise): a branch around it costs more in register
-        // copies than the multiplies do.
-        float mnew = m[rt];
-        if (__ballot(lm > m[rt] + kLazy)) {
-            const float mx = rowgroup_max(lm);
-            mnew = mx > m[rt] + kLazy ? mx : m[rt];
-        }
-        const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
-        m[rt] = mnew;
-        L[rt] *= alpha;
-        #pragma unroll
-        for (int e = 0; e < EPL; ++e) O[rt][e] *= alpha;
-        const float nm = (mnew == kNegInf) ? 0.f : -mnew;
+// Softmax pieces of the DMA path.  Scores are in log2 units once multiplied
+// by f (scale * log2 e).  A row's reference max m moves only when a score
+// passes it by kLazyDma; in between, exp2(x - m) stays below 2^kLazyDma, far
+// inside f32 / bf16 range, so the accumulators never need rescaling on the
+// common path.  The rare move (always the item's first pair, where m starts
+// at -inf) runs on a slow path outside the pair loop.
+constexpr float kLazyDma = 32.f;
+
+// Masks invalid tokens (PARTIAL) and returns the lane's max over the pair.
+template <int RT, bool PARTIAL>
+__device__ __forceinline__ float dma_lane_max(f4 (&s)[RT][2], int rt, int n0, int n1, int g, float f) {
+    f4& x0 = s[rt][0];
+    f4& x1 = s[rt][1];
+    if constexpr (PARTIAL) {
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            x0[i] = fast_exp2(__builtin_fmaf(x0[i], f, nm));
-            x1[i] = fast_exp2(__builtin_fmaf(x1[i], f, nm));
+            if (4 * g + i >= n0) x0[i] = kNegInf;
+            if (4 * g + i >= n1) x1[i] = kNegInf;
         }
-        pB[rt] = u32x4{pack2(x0[0], x0[1], F16), pack2(x0[2], x0[3], F16), pack2(x1[0], x1[1], F16),
-                       pack2(x1[2], x1[3], F16)};
-        L[rt] = mma16v<F16>(ones, pB[rt], L[rt]);
     }
+    return fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
+                 fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]))) * f;
+}
+
+// Probabilities of one tile with reference max m (packed for the PV MFMA),
+// and the row sums they add (MFMA against an all-ones operand).
+template <bool F16>
+__device__ __forceinline__ u32x4 dma_probs(const f4 (&x)[2], float f, float m, f4& L) {
+    const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
+    const u32x4 ones = {one2, one2, one2, one2};
+    const float nm = (m == kNegInf) ? 0.f : -m;
+    float p0[4], p1[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p0[i] = fast_exp2(__builtin_fmaf(x[0][i], f, nm));
+        p1[i] = fast_exp2(__builtin_fmaf(x[1][i], f, nm));
+    }
+    const u32x4 pb = {pack2(p0[0], p0[1], F16), pack2(p0[2], p0[3], F16), pack2(p1[0], p1[1], F16),
+                      pack2(p1[2], p1[3], F16)};
+    L = mma16v<F16>(ones, pb, L);
+    return pb;
 }
 
 struct DmaSrc {
@@ -959,54 +956,60 @@ __device__ __forceinline__ void dma_pair(const AttendArgs& a, const Item& it, co
     }
 }
 
-// The math of one page pair (slots s0 and s0 + PAGE of the ring).
-template <int D, bool F16, int NRT, bool TAIL>
-__device__ __forceinline__ void dma_pair_math(const AttendArgs& a, const uint8_t* s0, const LdsOffsets<D>& lo,
-                                              int n0, int n1, int g, const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
-                                              float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
-                                              f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+// Scores of the page pair in slots s0, s0 + PAGE for the wave's NRT tiles.
+template <int D, bool F16, int NRT>
+__device__ __forceinline__ void dma_scores(const uint8_t* s0, const LdsOffsets<D>& lo,
+                                           const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                           f4 (&sc)[DmaCfg<D>::RT][2]) {
     using C = DmaCfg<D>;
-    constexpr int RT = C::RT, KB = D / 32, EPL = D / 16;
+    constexpr int KB = D / 32;
     const uint8_t* s1 = s0 + C::PAGE;
-    f4 sc[RT][2];
-    {
-        u32x4 kop[2][KB];
+    u32x4 kop[2][KB];
+    #pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        kop[0][kb] = *reinterpret_cast<const u32x4*>(s0 + lo.k[kb]);
+        kop[1][kb] = *reinterpret_cast<const u32x4*>(s1 + lo.k[kb]);
+    }
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        sc[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
+        sc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-            kop[0][kb] = *reinterpret_cast<const u32x4*>(s0 + lo.k[kb]);
-            kop[1][kb] = *reinterpret_cast<const u32x4*>(s1 + lo.k[kb]);
-        }
-        #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            sc[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
-            sc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                sc[rt][0] = mma16v<F16>(kop[0][kb], qB[rt][kb], sc[rt][0]);
-                sc[rt][1] = mma16v<F16>(kop[1][kb], qB[rt][kb], sc[rt][1]);
-            }
+            sc[rt][0] = mma16v<F16>(kop[0][kb], qB[rt][kb], sc[rt][0]);
+            sc[rt][1] = mma16v<F16>(kop[1][kb], qB[rt][kb], sc[rt][1]);
         }
     }
-    u32x4 pB[RT];
-    const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
-    if (partial)
-        dma_softmax<F16, NRT, RT, EPL, true>(sc, n0, n1, a.scale_log2, m, Lsum, O, g, pB);
-    else
-        dma_softmax<F16, NRT, RT, EPL, false>(sc, n0, n1, a.scale_log2, m, Lsum, O, g, pB);
+}
+
+// The transposed V operands of the page pair in slots s0, s0 + PAGE, all
+// d-blocks at once (read before the scores so they land behind the MFMAs).
+template <int D>
+__device__ __forceinline__ void dma_v_operands(const uint8_t* s0, const LdsOffsets<D>& lo, u32x4 (&vop)[D / 16]) {
+    using C = DmaCfg<D>;
+    const uint8_t* s1 = s0 + C::PAGE;
     #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
+    for (int e = 0; e < D / 16; ++e) {
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s0 + lo.v[e]));
         const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s1 + lo.v[e]));
-        u32x4 vA = __builtin_shufflevector(__builtin_bit_cast(u32x2, v0), __builtin_bit_cast(u32x2, v1), 0, 1, 2,
-                                           3);
+        vop[e] = __builtin_shufflevector(__builtin_bit_cast(u32x2, v0), __builtin_bit_cast(u32x2, v1), 0, 1, 2, 3);
+    }
+}
+
+// O^T += V^T P^T with operands already in registers.
+template <int D, bool F16, int NRT, bool TAIL>
+__device__ __forceinline__ void dma_pv_regs(u32x4 (&vop)[D / 16], bool partial, int n0, int n1, int g,
+                                            const u32x4 (&pB)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+    #pragma unroll
+    for (int e = 0; e < D / 16; ++e) {
         if constexpr (TAIL) {
             if (partial) {
-                mask_v_tr(vA, 0, g, n0);
-                mask_v_tr(vA, 2, g, n1);
+                mask_v_tr(vop[e], 0, g, n0);
+                mask_v_tr(vop[e], 2, g, n1);
             }
         }
         #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vA, pB[rt], O[rt][e]);
+        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
     }
 }
 
@@ -1041,19 +1044,73 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
     const uint32_t pro = min(P - 1, npairs);
     #pragma unroll 1
     for (uint32_t q = 0; q < pro; ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
-    uint32_t ps = 0;
-    #pragma unroll 1
-    for (uint32_t pi = 0; pi < npairs; ++pi) {
-        // Issued so far: pairs < min(pi + P - 1, npairs); pair pi must have landed.
-        wait_vmcnt((min(pi + P - 1, npairs) - pi - 1) * C::PER_PAIR);
-        block_barrier();
-        if (pi + P - 1 < npairs)
-            dma_pair<D>(a, it, ids, src, ring_lds, pi + P - 1, ps == 0 ? P - 1 : ps - 1, wave);
-        const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
-        const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
-        if constexpr (NRT > 0)
-            dma_pair_math<D, F16, NRT, TAIL>(a, ring + ps * 2 * C::PAGE, lo, n0, n1, g, qB, m, Lsum, O);
+    uint32_t ps = 0, pi = 0;
+    constexpr int RT = C::RT;
+    const float f = a.scale_log2;
+    f4 sc[RT][2];
+    u32x4 vop[D / 16];
+    int n0 = kPageSize, n1 = kPageSize;
+    bool partial = false;
+    // Fast loop: pairs whose scores stay within kLazyDma of every row's
+    // reference max.  It leaves, with the pair's scores in sc, when a row
+    // needs its max moved; the slow path below handles that pair.
+    for (;;) {
+        bool moved = false;
+        #pragma unroll 1
+        for (; pi < npairs; ++pi) {
+            // Issued so far: pairs < min(pi + P - 1, npairs); pair pi must have landed.
+            wait_vmcnt((min(pi + P - 1, npairs) - pi - 1) * C::PER_PAIR);
+            block_barrier();
+            if (pi + P - 1 < npairs)
+                dma_pair<D>(a, it, ids, src, ring_lds, pi + P - 1, ps == 0 ? P - 1 : ps - 1, wave);
+            n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
+            n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
+            partial = (n0 != kPageSize) || (n1 != kPageSize);
+            if constexpr (NRT > 0) {
+                const uint8_t* s0 = ring + ps * 2 * C::PAGE;
+                dma_v_operands<D>(s0, lo, vop);
+                dma_scores<D, F16, NRT>(s0, lo, qB, sc);
+                bool need = false;
+                #pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) {
+                    const float lm = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
+                                             : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
+                    need |= lm > m[rt] + kLazyDma;
+                }
+                if (__ballot(need)) {
+                    moved = true;
+                    break;
+                }
+                u32x4 pB[RT];
+                #pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
+                dma_pv_regs<D, F16, NRT, TAIL>(vop, partial, n0, n1, g, pB, O);
+            }
+            ps = ps + 1 == P ? 0 : ps + 1;
+        }
+        if (!moved) break;
+        if constexpr (NRT > 0) {
+            // Slow path for pair pi: move each row's max to the pair's max
+            // where it passed the old one by kLazyDma, rescale that row's
+            // accumulators, then finish the pair.
+            #pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                const float lm = dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);   // already masked
+                const float mx = rowgroup_max(lm);
+                const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
+                const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+                m[rt] = mnew;
+                Lsum[rt] *= alpha;
+                #pragma unroll
+                for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
+            }
+            u32x4 pB[RT];
+            #pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
+            dma_pv_regs<D, F16, NRT, TAIL>(vop, partial, n0, n1, g, pB, O);
+        }
         ps = ps + 1 == P ? 0 : ps + 1;
+        ++pi;
     }
     // The last pair's wait was vmcnt(0): no ring load is outstanding.
 }
