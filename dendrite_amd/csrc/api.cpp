@@ -117,9 +117,10 @@ struct dh_plan {
     uint32_t pool_pages;
     uint32_t n_items;
     uint32_t n_tasks;
+    uint32_t n_group_items;
+    uint32_t n_wave_items;
     uint32_t n_slots;
     uint8_t* dev;
-    dh::Task* tasks;
     dh::Item* items;
     uint32_t* pages;
     dh::SeqSlot* seqslots;
@@ -514,15 +515,15 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     pl->pool_pages = pool->num_pages;
     pl->n_items = uint32_t(hp.items.size());
     pl->n_tasks = uint32_t(hp.tasks.size());
+    pl->n_group_items = hp.num_group_items;
+    pl->n_wave_items = hp.num_wave_items;
     pl->n_slots = hp.num_slots;
-    const size_t o_tasks = 0;
-    const size_t o_items = align_up(o_tasks + hp.tasks.size() * sizeof(dh::Task), 256);
+    const size_t o_items = 0;
     const size_t o_pages = align_up(o_items + hp.items.size() * sizeof(dh::Item), 256);
     const size_t o_ss = align_up(o_pages + hp.pages.size() * sizeof(uint32_t), 256);
     const size_t o_sp = align_up(o_ss + hp.seqslots.size() * sizeof(dh::SeqSlot), 256);
     const size_t total = align_up(o_sp + hp.slot_ptr.size() * sizeof(uint32_t), 256);
     std::vector<uint8_t> blob(total, 0);
-    memcpy(blob.data() + o_tasks, hp.tasks.data(), hp.tasks.size() * sizeof(dh::Task));
     memcpy(blob.data() + o_items, hp.items.data(), hp.items.size() * sizeof(dh::Item));
     memcpy(blob.data() + o_pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
     memcpy(blob.data() + o_ss, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
@@ -537,14 +538,15 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
         delete pl;
         return fail(DH_EHIP, "plan upload failed: %s", hipGetErrorString(e));
     }
-    pl->tasks = reinterpret_cast<dh::Task*>(pl->dev + o_tasks);
     pl->items = reinterpret_cast<dh::Item*>(pl->dev + o_items);
     pl->pages = reinterpret_cast<uint32_t*>(pl->dev + o_pages);
     pl->seqslots = reinterpret_cast<dh::SeqSlot*>(pl->dev + o_ss);
     pl->slot_ptr = reinterpret_cast<uint32_t*>(pl->dev + o_sp);
     const size_t rows = size_t(hp.num_slots) * cfg->num_heads;
-    pl->ws_lse_off = align_up(rows * cfg->head_dim * sizeof(float), 256);
-    pl->ws_bytes = align_up(pl->ws_lse_off + rows * sizeof(float), 256);
+    // Partial O: fp32 for f32 q, else f16 scaled per row (dh::PartialLse).
+    const size_t o_bytes = cfg->q_dtype == DH_DTYPE_F32 ? sizeof(float) : sizeof(uint16_t);
+    pl->ws_lse_off = align_up(rows * cfg->head_dim * o_bytes, 256);
+    pl->ws_bytes = align_up(pl->ws_lse_off + rows * sizeof(dh::PartialLse), 256);
     fill_stats(hp, batch, &pl->stats);
     retain(be);
     *out = pl;
@@ -592,11 +594,13 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
     if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
     DH_DEVICE(be->device);
     const dh_attn_config& c = pl->cfg;
-    float* ws_o = static_cast<float*>(ws);
-    float* ws_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
+    // Group items address query rows by 32-bit byte offsets into q.
+    if (uint64_t(pl->batch) * c.num_heads * c.head_dim * (c.q_dtype == DH_DTYPE_F32 ? 4u : 2u) > 0xFFFFFFFFull)
+        return fail(DH_EUNSUPPORTED, "q of %u x %u x %u exceeds 4 GiB", pl->batch, c.num_heads, c.head_dim);
+    void* ws_o = ws;
+    dh::PartialLse* ws_lse = reinterpret_cast<dh::PartialLse*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
     if (mask & 1u) {
         dh::AttendArgs a;
-        a.tasks = pl->tasks;
         a.items = pl->items;
         a.pages = pl->pages;
         a.seqslots = pl->seqslots;
@@ -611,6 +615,8 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         a.r = c.num_heads / c.num_kv_heads;
         a.gqa_tiled = c.gqa_mapping == DH_GQA_TILED ? 1u : 0u;
         a.scale_log2 = c.scale * 1.4426950408889634f;
+        a.n_group_items = pl->n_group_items;
+        a.n_wave_items = pl->n_wave_items;
         hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     }

@@ -156,6 +156,11 @@ __device__ __forceinline__ void row_target(const AttendArgs& a, const Item& it, 
     qh = a.gqa_tiled ? it.kv_head + j * a.hkv : it.kv_head * a.r + j;
 }
 
+// Item of wave `wave` in a workgroup past the group items (AttendArgs).
+__device__ __forceinline__ uint32_t wave_item_index(const AttendArgs& a, int wave) {
+    return a.n_group_items + (blockIdx.x - a.n_group_items) * kWaves + uint32_t(wave);
+}
+
 // Valid tokens of page index i of an item.
 __device__ __forceinline__ int page_tokens(const Item& it, uint32_t i, int last_len) {
     if (i >= it.npages) return 0;
@@ -172,31 +177,59 @@ __device__ __forceinline__ int item_last_len(const AttendArgs& a, const Item& it
     return (L <= 0 || L > kPageSize) ? kPageSize : L;
 }
 
+// Partial states: fp32 for f32 queries; otherwise f16, each row scaled by a
+// power of two 2^-k chosen from the row's largest magnitude (below 2^15
+// after scaling), so f16's range never clips and its 11-bit significand
+// holds every row at the same relative precision whatever the magnitude of
+// V.  k goes with the row's log2-sum-exp (PartialLse); the merge folds 2^k
+// into the row's weight, which is exact.
+__device__ __forceinline__ int partial_exp(float row_max_abs) {
+    if (!(row_max_abs > 0.f) || !(row_max_abs < 3.0e38f)) return 0;
+    return max(__builtin_amdgcn_frexp_expf(row_max_abs) - 15, -100);   // row_max_abs < 2^(k + 15)
+}
+
+template <int N>
+__device__ __forceinline__ void store_u32s(uint16_t* p, const uint32_t (&v)[N]) {
+    if constexpr (N % 4 == 0) {
+        #pragma unroll
+        for (int k = 0; k < N; k += 4)
+            *reinterpret_cast<u32x4*>(p + 2 * k) = u32x4{v[k], v[k + 1], v[k + 2], v[k + 3]};
+    } else if constexpr (N == 2) {
+        *reinterpret_cast<u32x2*>(p) = u32x2{v[0], v[1]};
+    } else {
+        static_assert(N == 1, "store width");
+        *reinterpret_cast<uint32_t*>(p) = v[0];
+    }
+}
+
 // Writes the partial states of one wave's rows: tiles rt < nrt, row
-// row0 + 16*rt + c of the item.  O[rt][e][i] is element d = (4g+i)*EPL + e.
-// lrow[rt]: the row's total weight when ROW_SUMMED, else this lane's share
-// (summed over the row's four lanes here).  TR: the accumulators come from
-// transposed V reads instead, O[rt][e][i] is element d = 16e + 4g + i.
-template <int D, int RT, bool ROW_SUMMED, bool TR = false>
+// row0 + 16*rt + c of the item, to partial rows dst[rt].  O[rt][e][i] is
+// element d = (4g+i)*EPL + e.  lrow[rt]: the row's total weight when
+// ROW_SUMMED, else this lane's share (summed over the row's four lanes here).
+template <int D, int RT, bool ROW_SUMMED, bool F32>
 __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const Item& it, uint32_t row0,
-                                                   int nrt, const float (&m)[RT], const float (&lrow)[RT],
-                                                   const f4 (&O)[RT][D / 16], int g, int c) {
+                                                   int nrt, const uint32_t (&dst)[RT], const float (&m)[RT],
+                                                   const float (&lrow)[RT], const f4 (&O)[RT][D / 16], int g,
+                                                   int c) {
     constexpr int EPL = D / 16;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         if (rt >= nrt) break;
         const float lt = ROW_SUMMED ? lrow[rt] : rowgroup_sum(lrow[rt]);
         const uint32_t row = row0 + rt * kTileRows + c;
-        if (row < it.nrows) {
-            uint32_t seq, slot, qh;
-            row_target(a, it, row, seq, slot, qh);
-            const uint32_t dst = slot * a.hq + qh;
-            const float inv = lt > 0.f ? 1.f / lt : 0.f;
-            float* o = a.ws_o + uint64_t(dst) * D;
-            if constexpr (TR) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        int k = 0;
+        if constexpr (!F32) {
+            float mx = 0.f;
+            #pragma unroll
+            for (int e = 0; e < EPL; ++e)
                 #pragma unroll
-                for (int e = 0; e < EPL; ++e) *reinterpret_cast<f4*>(o + 16 * e + 4 * g) = O[rt][e] * inv;
-            } else {
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(O[rt][e][i]));
+            k = partial_exp(rowgroup_max(mx) * inv);
+        }
+        if (row < it.nrows) {
+            if constexpr (F32) {
+                float* o = static_cast<float*>(a.ws_o) + uint64_t(dst[rt]) * D;
                 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     #pragma unroll
@@ -206,8 +239,18 @@ __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const It
                         *reinterpret_cast<f4*>(o + (4 * g + i) * EPL + e) = v;
                     }
                 }
+            } else {
+                const float sc = __builtin_amdgcn_ldexpf(inv, -k);
+                uint16_t* o = static_cast<uint16_t*>(a.ws_o) + uint64_t(dst[rt]) * D;
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t v[EPL / 2];
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e += 2) v[e / 2] = pack2(O[rt][e][i] * sc, O[rt][e + 1][i] * sc, true);
+                    store_u32s<EPL / 2>(o + (4 * g + i) * EPL, v);
+                }
             }
-            if (g == 0) a.ws_lse[dst] = lt > 0.f ? m[rt] + log2f(lt) : kNegInf;
+            if (g == 0) a.ws_lse[dst[rt]] = PartialLse{lt > 0.f ? m[rt] + log2f(lt) : kNegInf, float(k)};
         }
     }
 }
@@ -216,14 +259,16 @@ __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const It
 // dims kb*32 + 8g .. +8 (zero for rows outside the item).
 template <int D, int RT>
 __device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, uint32_t row0, int nrt,
-                                         uint32_t (&qB)[RT][D / 32][4], int g, int c) {
+                                         uint32_t (&qB)[RT][D / 32][4], uint32_t (&dst)[RT], int g, int c) {
     constexpr int KB = D / 32;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const uint32_t row = row0 + rt * kTileRows + c;
+        dst[rt] = 0u;
         if (rt < nrt && row < it.nrows) {
             uint32_t seq, slot, qh;
             row_target(a, it, row, seq, slot, qh);
+            dst[rt] = slot * a.hq + qh;
             const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
             #pragma unroll
             for (int kb = 0; kb < KB; ++kb) load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
@@ -453,7 +498,8 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
     constexpr int KB = D / 32;
     constexpr bool BLOCK_SCALE = (KVF == KVF_FP8);
     uint32_t qB[1][KB][4];
-    load_q16<D, 1>(a, it, 0, 1, qB, g, c);
+    uint32_t dst[1];
+    load_q16<D, 1>(a, it, 0, 1, qB, dst, g, c);
     float m[1] = {kNegInf};
     f4 L[1] = {f4{0.f, 0.f, 0.f, 0.f}};
     f4 O[1][EPL];
@@ -523,7 +569,7 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
         }
     }
     const float lr[1] = {L[0][0]};
-    write_wave_partial<D, 1, true>(a, it, 0, 1, m, lr, O, g, c);
+    write_wave_partial<D, 1, true, false>(a, it, 0, 1, dst, m, lr, O, g, c);
 }
 
 // ------------------------------------------------------------ group items
@@ -732,7 +778,8 @@ __device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, 
     const uint32_t row0 = uint32_t(wave) * RT * kTileRows;
     const int nrt = it.nrows > row0 ? min(RT, int((it.nrows - row0 + kTileRows - 1) / kTileRows)) : 0;
     uint32_t qB[RT][KB][4];
-    load_q16<D, RT>(a, it, row0, nrt, qB, g, c);
+    uint32_t dst[RT];
+    load_q16<D, RT>(a, it, row0, nrt, qB, dst, g, c);
     float m[RT];
     f4 L[RT];
     f4 O[RT][EPL];
@@ -749,17 +796,25 @@ __device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, 
     float lr[RT];
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) lr[rt] = L[rt][0];
-    write_wave_partial<D, RT, true>(a, it, row0, nrt, m, lr, O, g, c);
+    write_wave_partial<D, RT, true, false>(a, it, row0, nrt, dst, m, lr, O, g, c);
 }
 
 // ------------------------------------------------- group items, 16-bit KV
 // Pages reach LDS by direct global->LDS loads (global_load_lds_dwordx4, one
 // 1 KiB wave load per 64 lanes x 16 bytes): no staging registers and no
-// VALU work.  The ring is two LDS objects ("halves") of H page pairs each:
-// while the waves compute the H pairs of one half, the loads of the next H
-// pairs fill the other.  Because the halves are distinct objects the
-// compiler tracks which loads each read depends on and waits exactly; the
-// explicit waits before each barrier make every wave's loads visible to all.
+// VALU work.  The LDS ring holds NP page pairs; pair p goes to slot p % NP.
+// The loads are issued from inline assembly, so the compiler tracks none of
+// them and inserts no wait of its own on the ring: before pair p is read
+// each wave waits (vmcnt) until its own loads of pair p have landed, and the
+// barrier that follows makes every wave's share of the pair visible.  After
+// that barrier the slot of pair p - 1 is free and takes pair p + NP - 1.
+//
+// The item's query rows take the same route: at the start each wave loads
+// its rows into the last QSLOTS slots (lane l of a wave load receives bytes
+// 16 l.., so each lane reads its own MFMA operand back), then reads them to
+// registers; a barrier frees those slots for pages.  The page ids, the row
+// targets and the query rows thus cost one dependent memory round trip each
+// at the start of an item instead of a chain of them.
 //
 // A slot holds one page: the K plane (16 rows) then the V plane.  The
 // 16-byte chunks of row r are XOR-swizzled (chunk j at position j ^ swz(r)),
@@ -769,7 +824,7 @@ __device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, 
 //   row 4g + c/4 at dims 16e + 4(c%4); within each 16-lane group the
 //   transpose hands lane c the values V[4g + j][16e + c], j = 0..3 — the
 //   MFMA's k = 4g + j slots — so the accumulators hold O[row][16e + 4g + i].
-// Each wave owns row tiles w, w+4, w+8, w+12 of the item (up to 256 rows).
+// Each wave owns row tiles w, w+4 (RT = 2; one tile for D = 256) of the item.
 template <int D>
 struct DmaCfg {
     static constexpr int RB = 2 * D;                  // bytes per row
@@ -780,6 +835,9 @@ struct DmaCfg {
     static constexpr int DPP = PAGE / (kWaves * 64 * 16);   // wave loads per thread per page
     static constexpr int PER_PAIR = 2 * DPP;          // loads per thread per pair
     static constexpr int RT = group_tiles16(D);       // row tiles per wave
+    static constexpr int QBYTES = kWaves * RT * (D / 32) * 1024;   // the item's query rows
+    static constexpr int QSLOTS = (QBYTES + 2 * PAGE - 1) / (2 * PAGE);
+    static_assert(NP - QSLOTS >= 2, "query rows leave two pair slots");
     static_assert(DPP >= 1 && PLANE % 1024 == 0, "a page must split into 1 KiB wave loads");
     static_assert(NP >= 3 && (NP - 2) * PER_PAIR <= 48, "vmcnt cases");
     static_assert(DPP <= 4, "DmaSrc holds four offsets");
@@ -1013,15 +1071,40 @@ __device__ __forceinline__ void dma_pv_regs(u32x4 (&vop)[D / 16], bool partial, 
     }
 }
 
+// Where the rows of a wave's tiles come from and go to: the byte offset of
+// the query row in q and the partial-state row, read once per item.  Rows
+// past the item's last are given its last row (their query is zeroed and
+// nothing is written for them).
+template <int RT>
+struct RowTargets {
+    uint32_t qoff[RT];
+    uint32_t dst[RT];
+};
+
+template <int D, int RT>
+__device__ __forceinline__ void dma_row_targets(const AttendArgs& a, const Item& it, int wave, int c,
+                                                RowTargets<RT>& rtg) {
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
+        row = row < it.nrows ? row : it.nrows - 1;
+        uint32_t seq, slot, qh;
+        row_target(a, it, row, seq, slot, qh);
+        rtg.qoff[rt] = (seq * a.hq + qh) * uint32_t(D * 2);
+        rtg.dst[rt] = slot * a.hq + qh;
+    }
+}
+
 template <int D, bool F16, int NRT, bool TAIL>
 __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                uint8_t* ring, int tid, int wave, int g, int c,
-                                               const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                               const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
+                                               u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
                                                float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
                                                f4 (&O)[DmaCfg<D>::RT][D / 16]) {
     using C = DmaCfg<D>;
-    constexpr uint32_t P = C::NP;
-    const int last_len = TAIL ? item_last_len(a, it) : kPageSize;
+    constexpr uint32_t P = C::NP, QS = C::QSLOTS;
+    constexpr int KB = D / 32;
     const uint32_t np = it.npages;
     const uint32_t npairs = (np + 1) >> 1;
     DmaSrc src;
@@ -1036,14 +1119,38 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
     }
     const LdsOffsets<D> lo = lds_offsets<D>(g, c);
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
-    // Every load the compiler issued (the query rows, the last page length)
-    // lands before the ring loads start, so the loop holds no compiler-tracked
-    // load and no compiler-inserted wait can drain the ring.
+    // Every load the compiler issued (row targets, page ids) has landed
+    // before the ring loads start, so no compiler-inserted wait can drain
+    // the ring.
     __builtin_amdgcn_s_waitcnt(0x0070);
     compiler_fence();
-    const uint32_t pro = min(P - 1, npairs);
+    // Query rows into the last QS slots, the first pairs into the others.
+    const uint32_t q_lds = ring_lds + (P - QS) * 2 * C::PAGE + wave * (C::RT * KB * 1024);
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        #pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+            dma_x4(q_lds + (rt * KB + kb) * 1024, static_cast<const uint8_t*>(a.q), rtg.qoff[rt] + kb * 64 + 16 * g);
+    }
+    const uint32_t pro = min(P - QS, npairs);
     #pragma unroll 1
     for (uint32_t q = 0; q < pro; ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
+    wait_vmcnt(pro * C::PER_PAIR);   // loads land in issue order: the query rows are in
+    if constexpr (NRT > 0) {
+        const uint8_t* qw = ring + (P - QS) * 2 * C::PAGE + wave * (C::RT * KB * 1024) + 16 * (tid & 63);
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const bool valid = uint32_t(rt * kWaves + wave) * kTileRows + c < it.nrows;
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024);
+                qB[rt][kb] = valid ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+    block_barrier();   // every wave holds its query rows: their slots take pages
+    #pragma unroll 1
+    for (uint32_t q = pro; q < min(P - 1, npairs); ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
     uint32_t ps = 0, pi = 0;
     constexpr int RT = C::RT;
     const float f = a.scale_log2;
@@ -1118,55 +1225,42 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
 // Query rows of a wave's tiles in a DMA group item: tile rt of wave w covers
 // rows (rt * kWaves + w) * 16 .. +16.
 template <int D, int RT>
-__device__ __forceinline__ void load_q_dma(const AttendArgs& a, const Item& it, int wave, int g, int c,
-                                           u32x4 (&qB)[RT][D / 32]) {
-    constexpr int KB = D / 32;
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
-        if (row < it.nrows) {
-            uint32_t seq, slot, qh;
-            row_target(a, it, row, seq, slot, qh);
-            const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) qB[rt][kb] = *reinterpret_cast<const u32x4*>(qp + kb * 32 + 8 * g);
-        } else {
-            #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) qB[rt][kb] = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-}
-
-template <int D, int RT>
 __device__ __forceinline__ void write_partial_dma(const AttendArgs& a, const Item& it, int wave, int nrt,
-                                                  const float (&m)[RT], const f4 (&L)[RT],
-                                                  const f4 (&O)[RT][D / 16], int g, int c) {
+                                                  const uint32_t (&dst)[RT], const float (&m)[RT],
+                                                  const f4 (&L)[RT], const f4 (&O)[RT][D / 16], int g, int c) {
     constexpr int EPL = D / 16;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         if (rt >= nrt) break;
         const uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
-        if (row < it.nrows) {
-            uint32_t seq, slot, qh;
-            row_target(a, it, row, seq, slot, qh);
-            const uint32_t dst = slot * a.hq + qh;
-            const float lt = L[rt][0];
-            const float inv = lt > 0.f ? 1.f / lt : 0.f;
-            float* o = a.ws_o + uint64_t(dst) * D;
+        const float lt = L[rt][0];
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        float mx = 0.f;
+        #pragma unroll
+        for (int e = 0; e < EPL; ++e)
             #pragma unroll
-            for (int e = 0; e < EPL; ++e) *reinterpret_cast<f4*>(o + 16 * e + 4 * g) = O[rt][e] * inv;
-            if (g == 0) a.ws_lse[dst] = lt > 0.f ? m[rt] + log2f(lt) : kNegInf;
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(O[rt][e][i]));
+        const int k = partial_exp(rowgroup_max(mx) * inv);
+        const float sc = __builtin_amdgcn_ldexpf(inv, -k);
+        if (row < it.nrows) {
+            uint16_t* o = static_cast<uint16_t*>(a.ws_o) + uint64_t(dst[rt]) * D;
+            #pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const f4 v = O[rt][e] * sc;
+                *reinterpret_cast<u32x2*>(o + 16 * e + 4 * g) = u32x2{pack2(v[0], v[1], true), pack2(v[2], v[3], true)};
+            }
+            if (g == 0) a.ws_lse[dst[rt]] = PartialLse{lt > 0.f ? m[rt] + log2f(lt) : kNegInf, float(k)};
         }
     }
 }
 
 template <int D, bool F16, int NRT>
 __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
-                                              uint8_t* ring, int tid, int wave, int g, int c) {
+                                              uint8_t* ring, int tid, int wave, int g, int c,
+                                              const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
     using C = DmaCfg<D>;
     constexpr int RT = C::RT, EPL = D / 16, KB = D / 32;
     u32x4 qB[RT][KB];
-    load_q_dma<D, RT>(a, it, wave, g, c, qB);
     float m[RT];
     f4 L[RT];
     f4 O[RT][EPL];
@@ -1178,10 +1272,10 @@ __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& i
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
     if (it.flags & kItemTail)
-        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, qB, m, L, O);
+        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
     else
-        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, qB, m, L, O);
-    write_partial_dma<D, RT>(a, it, wave, NRT, m, L, O, g, c);
+        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
+    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, m, L, O, g, c);
 }
 
 // Item fields as wave-uniform values (they are: the item is the workgroup's),
@@ -1206,15 +1300,19 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
     __shared__ __attribute__((aligned(1024))) uint8_t ring[C::RING];
     __shared__ uint32_t ids[kGroupMaxPages];
     const Item it = uniform_item(item);
+    // Row targets, the last page's length and the page ids load together.
+    RowTargets<C::RT> rtg;
+    dma_row_targets<D, C::RT>(a, it, wave, c, rtg);
+    const int last_len = item_last_len(a, it);
     for (uint32_t i = tid; i < it.npages; i += kWaves * 64) ids[i] = a.pages[it.page_off + i];
     __syncthreads();
     // Tiles of this wave that hold rows: tiles w, w+4, ... below ceil(nrows/16).
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
-    if (nrt >= 3) dma_group_run<D, F16, C::RT>(a, it, ids, ring, tid, wave, g, c);
-    else if (nrt == 2) dma_group_run<D, F16, 2>(a, it, ids, ring, tid, wave, g, c);
-    else if (nrt == 1) dma_group_run<D, F16, 1>(a, it, ids, ring, tid, wave, g, c);
-    else dma_group_run<D, F16, 0>(a, it, ids, ring, tid, wave, g, c);
+    if (nrt >= 3) dma_group_run<D, F16, C::RT>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 2) dma_group_run<D, F16, 2>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 1) dma_group_run<D, F16, 1>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else dma_group_run<D, F16, 0>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
 }
 
 // ---------------------------------------------------------------- attend16
@@ -1225,14 +1323,13 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     // Wave index as a wave-uniform (scalar) value: page-list reads then go
     // through the scalar cache and never wait on the vector loads in flight.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const Task t = a.tasks[blockIdx.x];
-    if (t.kind == kTaskGroup) {
-        const Item it = a.items[t.first];
+    if (blockIdx.x < a.n_group_items) {
+        const Item it = a.items[blockIdx.x];
         if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
         else group_item_dma<D, F16>(a, it, tid, wave, g, c);
-    } else if (uint32_t(wave) < t.count) {
-        const Item it = a.items[t.first + wave];
-        wave_item<D, KVF, F16>(a, it, g, c);
+    } else {
+        const uint32_t idx = wave_item_index(a, wave);
+        if (idx < a.n_group_items + a.n_wave_items) wave_item<D, KVF, F16>(a, a.items[idx], g, c);
     }
 }
 
@@ -1247,14 +1344,16 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     constexpr int EPL = D / 16;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const Task t = a.tasks[blockIdx.x];
-    if (uint32_t(wave) >= t.count) return;
-    const Item it = a.items[t.first + wave];
+    const uint32_t idx = wave_item_index(a, wave);
+    if (idx >= a.n_group_items + a.n_wave_items) return;
+    const Item it = a.items[idx];
 
     float qv[KQ];
+    uint32_t dst[1] = {0u};
     if (uint32_t(c) < it.nrows) {
         uint32_t seq, slot, qh;
         row_target(a, it, c, seq, slot, qh);
+        dst[0] = slot * a.hq + qh;
         const float* qp = reinterpret_cast<const float*>(a.q) + (uint64_t(seq) * a.hq + qh) * D + g * KQ;
         load_dwords<KQ>(reinterpret_cast<uint32_t*>(qv), qp);
     } else {
@@ -1317,7 +1416,7 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
                 O[0][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i][e], x[i], O[0][e], 0, 0, 0);
         }
     }
-    write_wave_partial<D, 1, false>(a, it, 0, 1, m, l, O, g, c);
+    write_wave_partial<D, 1, false, true>(a, it, 0, 1, dst, m, l, O, g, c);
 }
 
 // ------------------------------------------------------------------ merge
@@ -1339,6 +1438,29 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// PL consecutive partial-O elements starting at element e of the partial
+// rows: fp32 when the output is f32 (OUT == 2), else scaled f16.
+template <int OUT, int PL>
+__device__ __forceinline__ void load_partial(const void* ws, uint64_t e, float (&v)[PL]) {
+    if constexpr (OUT == 2) {
+        const float* o = static_cast<const float*>(ws) + e;
+        #pragma unroll
+        for (int q = 0; q < PL; ++q) v[q] = o[q];
+    } else if constexpr (PL == 1) {
+        v[0] = float(static_cast<const _Float16*>(ws)[e]);
+    } else {
+        const uint32_t* o = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(ws) + e);
+        uint32_t w[PL / 2];
+        #pragma unroll
+        for (int q = 0; q < PL / 2; ++q) w[q] = o[q];
+        #pragma unroll
+        for (int q = 0; q < PL / 2; ++q) {
+            v[2 * q] = unpack_lo(w[q], true);
+            v[2 * q + 1] = unpack_hi(w[q], true);
+        }
+    }
+}
+
 template <int D, uint32_t OUT>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     constexpr int PL = D / 64;
@@ -1349,7 +1471,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
     const uint32_t s0 = a.slot_ptr[b], n = a.slot_ptr[b + 1] - s0;
     float M = kNegInf;
-    for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh]);
+    for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh].lse);
     M = wave_max(M);
     float acc[PL];
     #pragma unroll
@@ -1359,22 +1481,21 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         for (uint32_t base = 0; base < n; base += 64) {
             // Weight of slot base + lane, then the slots' O rows in groups of U.
             const uint32_t k = base + lane;
-            const float Lk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : kNegInf;
-            const float wk = Lk == kNegInf ? 0.f : fast_exp2(Lk - M);
+            const PartialLse pk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : PartialLse{kNegInf, 0.f};
+            const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
             W += wk;
+            const float wo = __builtin_amdgcn_ldexpf(wk, int(pk.k));   // weight of the stored (scaled) O
             const uint32_t cnt = min(64u, n - base);
             for (uint32_t j0 = 0; j0 < cnt; j0 += U) {
                 float v[U][PL];
                 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const uint32_t j = min(j0 + u, cnt - 1);
-                    const float* o = a.ws_o + (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL;
-                    #pragma unroll
-                    for (int q = 0; q < PL; ++q) v[u][q] = o[q];
+                    load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL, v[u]);
                 }
                 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const float w = (j0 + u < cnt) ? __shfl(wk, int(j0 + u), 64) : 0.f;
+                    const float w = (j0 + u < cnt) ? __shfl(wo, int(j0 + u), 64) : 0.f;
                     #pragma unroll
                     for (int q = 0; q < PL; ++q) acc[q] += w * v[u][q];
                 }

@@ -66,8 +66,17 @@ struct SeqSlot {
     uint32_t slot;
 };
 
+// Per partial row: its log2-sum-exp of scaled scores and the power of two k
+// its stored O carries (stored = O * 2^-k; k = 0 for fp32 partials).
+struct PartialLse {
+    float lse;
+    float k;
+};
+
+// Workgroup b runs group item b when b < n_group_items; otherwise it runs the
+// wave items n_group_items + 4 (b - n_group_items) + w, one per wave w, that
+// exist (the planner emits its tasks in exactly this order).
 struct AttendArgs {
-    const Task* tasks;
     const Item* items;
     const uint32_t* pages;
     const SeqSlot* seqslots;
@@ -75,16 +84,18 @@ struct AttendArgs {
     const uint8_t* kv;           // pool data [P][2][Hkv][16][D]
     const void* scales;          // pool scale records (format dependent)
     const int32_t* last_page_len;
-    float* ws_o;                 // [slots][Hq][D] normalised partial O
-    float* ws_lse;               // [slots][Hq] log2-sum-exp of scaled scores
+    void* ws_o;                  // [slots][Hq][D] normalised partial O: fp32 for f32 q,
+                                 // else f16 scaled per row by 2^-k
+    PartialLse* ws_lse;          // [slots][Hq]
     uint32_t hq, hkv, r, gqa_tiled;
     float scale_log2;            // softmax scale * log2(e)
+    uint32_t n_group_items, n_wave_items;
 };
 
 struct MergeArgs {
     const uint32_t* slot_ptr;    // [B+1] partial slots of sequence b
-    const float* ws_o;
-    const float* ws_lse;
+    const void* ws_o;            // as AttendArgs::ws_o
+    const PartialLse* ws_lse;
     void* out;                   // [B][Hq][D]
     uint32_t batch, hq;
 };

@@ -293,6 +293,20 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     }
     out.num_group_items = uint32_t(gorder.size());
     out.num_wave_items = uint32_t(waves.size());
+    // The attention kernel derives a workgroup's items from its index alone
+    // (AttendArgs): group task b runs item b, wave task b runs items
+    // G + 4 (b - G) + w.  Check the emitted tasks against that mapping.
+    for (size_t b = 0; b < out.tasks.size(); ++b) {
+        const Task& t = out.tasks[b];
+        const uint32_t G = out.num_group_items;
+        const bool ok = b < G ? (t.kind == kTaskGroup && t.first == b && t.count == 1)
+                              : (t.kind == kTaskWaves && t.first == G + kWaves * uint32_t(b - G) &&
+                                 t.count == std::min<uint32_t>(kWaves, out.num_wave_items - kWaves * uint32_t(b - G)));
+        if (!ok) {
+            err = "internal: task " + std::to_string(b) + " does not follow the workgroup-to-item mapping";
+            return DH_EINVAL;
+        }
+    }
     return DH_OK;
 }
 
