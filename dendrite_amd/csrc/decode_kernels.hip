@@ -843,10 +843,15 @@ struct DmaCfg {
     static_assert(DPP <= 4, "DmaSrc holds four offsets");
 };
 
+// Row swizzle of the 16-byte chunks.  Both read patterns were measured on
+// gfx950 (SQ_LDS_BANK_CONFLICT, one probe kernel per pattern): these values
+// leave the K reads (ds_read_b128) and the transposed V reads
+// (ds_read_b64_tr_b16) without bank conflicts at head_dim 64, 128 and 256.
+// Setting bit 0 from row >> 3 as well makes the K reads two-way conflicted.
 template <int D>
 __device__ __forceinline__ int chunk_swz(int row) {
-    if constexpr (D == 64) return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
-    else return ((row & 7) << 1) | (row >> 3);
+    if constexpr (D == 64) return ((row >> 1) & 3) << 1;
+    else return (row & 7) << 1;
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -897,6 +902,12 @@ __device__ __forceinline__ void wait_vmcnt(uint32_t n) {
     }
 }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_const() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Barrier after this wave's LDS reads have returned (lgkmcnt(0)), so no
 // read of a slot can still be in flight when another wave refills it.
 __device__ __forceinline__ void block_barrier() {
@@ -906,26 +917,28 @@ __device__ __forceinline__ void block_barrier() {
     compiler_fence();
 }
 
-// Lane byte offsets inside a slot of the K operand reads (per k-block) and
-// the transposed V reads (per d-block).
-template <int D>
+// Lane byte offsets inside a slot of the K operand read of k-block 0 and
+// the transposed V read of d-block 0.  The swizzle is an XOR on the chunk
+// index (bits 4.. of the offset) and slots start at multiples of 1 KiB, so
+// k-block kb is at (slot + k) ^ (kb << 6) and d-block e at (slot + v) ^ (e << 5):
+// chunk 4kb + g -> (4kb + g) ^ swz = 4 (kb ^ (swz >> 2)) + (g ^ (swz & 3)), and
+// chunk 2e + h likewise.  Two registers instead of one per block.
 struct LdsOffsets {
-    uint32_t k[D / 32];
-    uint32_t v[D / 16];
+    uint32_t k;
+    uint32_t v;
 };
 
 template <int D>
-__device__ __forceinline__ LdsOffsets<D> lds_offsets(int g, int c) {
+__device__ __forceinline__ LdsOffsets lds_offsets(int g, int c) {
     using C = DmaCfg<D>;
-    LdsOffsets<D> o;
-    #pragma unroll
-    for (int kb = 0; kb < D / 32; ++kb) o.k[kb] = c * C::RB + (((4 * kb + g) ^ chunk_swz<D>(c)) << 4);
+    LdsOffsets o;
+    o.k = c * C::RB + ((g ^ chunk_swz<D>(c)) << 4);
     const int row = 4 * g + (c >> 2);
-    #pragma unroll
-    for (int e = 0; e < D / 16; ++e)
-        o.v[e] = C::PLANE + row * C::RB + (((2 * e + ((c & 3) >> 1)) ^ chunk_swz<D>(row)) << 4) + ((c & 1) << 3);
+    o.v = C::PLANE + row * C::RB + ((((c & 3) >> 1) ^ chunk_swz<D>(row)) << 4) + ((c & 1) << 3);
     return o;
 }
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
 // Zeroes the V values of tokens 4g + j >= n (j = 0..3) in one page's half
 // (dwords w0, w0+1) of a transposed V operand.
@@ -997,6 +1010,20 @@ __device__ __forceinline__ void dma_x4(uint32_t lds, const void* gbase, uint32_t
                  : "memory", "m0");
 }
 
+// Issues this wave's share of the loads of pages pg0, pg1 into pair slot `ps`.
+template <int D>
+__device__ __forceinline__ void dma_pair_pages(const AttendArgs& a, uint32_t pg0, uint32_t pg1, const DmaSrc& src,
+                                               uint32_t ring, uint32_t ps, int wave) {
+    using C = DmaCfg<D>;
+    #pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint8_t* base = a.kv + uint64_t(q == 0 ? pg0 : pg1) * src.page_stride;
+        const uint32_t slot = ring + (2 * ps + q) * C::PAGE + wave * C::DPP * 1024;
+        #pragma unroll
+        for (int u = 0; u < C::DPP; ++u) dma_x4(slot + u * 1024, base, src.loff[u]);
+    }
+}
+
 // Issues this wave's share of the loads of pair `pair` into pair slot `ps`.
 template <int D>
 __device__ __forceinline__ void dma_pair(const AttendArgs& a, const Item& it, const uint32_t* ids,
@@ -1014,42 +1041,57 @@ __device__ __forceinline__ void dma_pair(const AttendArgs& a, const Item& it, co
     }
 }
 
-// Scores of the page pair in slots s0, s0 + PAGE for the wave's NRT tiles.
-template <int D, bool F16, int NRT>
-__device__ __forceinline__ void dma_scores(const uint8_t* s0, const LdsOffsets<D>& lo,
-                                           const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
-                                           f4 (&sc)[DmaCfg<D>::RT][2]) {
+// K operands of the page pair in slots s0, s0 + PAGE (LDS byte address).
+template <int D>
+__device__ __forceinline__ void dma_k_operands(uint32_t s0, const LdsOffsets& lo, u32x4 (&kop)[2][D / 32]) {
     using C = DmaCfg<D>;
-    constexpr int KB = D / 32;
-    const uint8_t* s1 = s0 + C::PAGE;
-    u32x4 kop[2][KB];
+    const uint32_t k0 = s0 + lo.k;
     #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-        kop[0][kb] = *reinterpret_cast<const u32x4*>(s0 + lo.k[kb]);
-        kop[1][kb] = *reinterpret_cast<const u32x4*>(s1 + lo.k[kb]);
+    for (int kb = 0; kb < D / 32; ++kb) {
+        const uint32_t ad = k0 ^ uint32_t(kb << 6);
+        kop[0][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(ad));
+        kop[1][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(ad + C::PAGE));
     }
+}
+
+// Scores of a page pair for the wave's NRT tiles from its K operands.
+template <int D, bool F16, int NRT>
+__device__ __forceinline__ void dma_score_mma(const u32x4 (&kop)[2][D / 32],
+                                              const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                              f4 (&sc)[DmaCfg<D>::RT][2]) {
     #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
         sc[rt][0] = f4{0.f, 0.f, 0.f, 0.f};
         sc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < D / 32; ++kb) {
             sc[rt][0] = mma16v<F16>(kop[0][kb], qB[rt][kb], sc[rt][0]);
             sc[rt][1] = mma16v<F16>(kop[1][kb], qB[rt][kb], sc[rt][1]);
         }
     }
 }
 
+// Scores of the page pair in slots s0, s0 + PAGE for the wave's NRT tiles.
+template <int D, bool F16, int NRT>
+__device__ __forceinline__ void dma_scores(uint32_t s0, const LdsOffsets& lo,
+                                           const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                           f4 (&sc)[DmaCfg<D>::RT][2]) {
+    u32x4 kop[2][D / 32];
+    dma_k_operands<D>(s0, lo, kop);
+    dma_score_mma<D, F16, NRT>(kop, qB, sc);
+}
+
 // The transposed V operands of the page pair in slots s0, s0 + PAGE, all
 // d-blocks at once (read before the scores so they land behind the MFMAs).
 template <int D>
-__device__ __forceinline__ void dma_v_operands(const uint8_t* s0, const LdsOffsets<D>& lo, u32x4 (&vop)[D / 16]) {
+__device__ __forceinline__ void dma_v_operands(uint32_t s0, const LdsOffsets& lo, u32x4 (&vop)[D / 16]) {
     using C = DmaCfg<D>;
-    const uint8_t* s1 = s0 + C::PAGE;
+    const uint32_t v00 = s0 + lo.v;
     #pragma unroll
     for (int e = 0; e < D / 16; ++e) {
-        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s0 + lo.v[e]));
-        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(s1 + lo.v[e]));
+        const uint32_t ad = v00 ^ uint32_t(e << 5);
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(ad));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(ad + C::PAGE));
         vop[e] = __builtin_shufflevector(__builtin_bit_cast(u32x2, v0), __builtin_bit_cast(u32x2, v1), 0, 1, 2, 3);
     }
 }
@@ -1117,7 +1159,7 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
         const int j = pos ^ chunk_swz<D>(row);
         src.loff[u] = uint32_t((plane * a.hkv + it.kv_head) * C::PLANE + row * C::RB + j * 16);
     }
-    const LdsOffsets<D> lo = lds_offsets<D>(g, c);
+    const LdsOffsets lo = lds_offsets<D>(g, c);
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
     // Every load the compiler issued (row targets, page ids) has landed
     // before the ring loads start, so no compiler-inserted wait can drain
@@ -1151,73 +1193,108 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
     block_barrier();   // every wave holds its query rows: their slots take pages
     #pragma unroll 1
     for (uint32_t q = pro; q < min(P - 1, npairs); ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
-    uint32_t ps = 0, pi = 0;
+    // Software pipeline: iteration pi computes the scores of pair pi + 1
+    // while it finishes pair pi.  It reads K of pair pi + 1 and V of pair
+    // pi; after its barrier the slot of pair pi - 1 is free and takes pair
+    // pi + P - 1.  Issued before iteration pi: pairs < min(pi + P - 1, npairs).
+    // Order inside an iteration (pinned with scheduling barriers, since a
+    // wave issues in order): the row-max check of pair pi (its scores are
+    // already in registers) and the rare rescale; then all LDS reads; then
+    // the probabilities of pair pi (VALU), which cover the LDS latency; then
+    // the score MFMAs of pair pi + 1 and the PV MFMAs of pair pi.
     constexpr int RT = C::RT;
     const float f = a.scale_log2;
     f4 sc[RT][2];
     u32x4 vop[D / 16];
-    int n0 = kPageSize, n1 = kPageSize;
-    bool partial = false;
-    // Fast loop: pairs whose scores stay within kLazyDma of every row's
-    // reference max.  It leaves, with the pair's scores in sc, when a row
-    // needs its max moved; the slow path below handles that pair.
-    for (;;) {
-        bool moved = false;
-        #pragma unroll 1
-        for (; pi < npairs; ++pi) {
-            // Issued so far: pairs < min(pi + P - 1, npairs); pair pi must have landed.
-            wait_vmcnt((min(pi + P - 1, npairs) - pi - 1) * C::PER_PAIR);
-            block_barrier();
-            if (pi + P - 1 < npairs)
-                dma_pair<D>(a, it, ids, src, ring_lds, pi + P - 1, ps == 0 ? P - 1 : ps - 1, wave);
-            n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
-            n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
-            partial = (n0 != kPageSize) || (n1 != kPageSize);
-            if constexpr (NRT > 0) {
-                const uint8_t* s0 = ring + ps * 2 * C::PAGE;
-                dma_v_operands<D>(s0, lo, vop);
-                dma_scores<D, F16, NRT>(s0, lo, qB, sc);
-                bool need = false;
-                #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) {
-                    const float lm = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
-                                             : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
-                    need |= lm > m[rt] + kLazyDma;
-                }
-                if (__ballot(need)) {
-                    moved = true;
-                    break;
-                }
-                u32x4 pB[RT];
-                #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
-                dma_pv_regs<D, F16, NRT, TAIL>(vop, partial, n0, n1, g, pB, O);
-            }
-            ps = ps + 1 == P ? 0 : ps + 1;
+    wait_vmcnt((min(P - 1, npairs) - 1) * C::PER_PAIR);   // pair 0 has landed
+    block_barrier();
+    if constexpr (NRT > 0) dma_scores<D, F16, NRT>(ring_lds, lo, qB, sc);
+    uint32_t ps = 0, psn = 1;   // slots of pairs pi, pi + 1
+    // Page ids of the pair the next refill loads (pair pi + P - 1), read from
+    // LDS an iteration ahead so the refill does not wait on them.
+    uint32_t nid0 = 0, nid1 = 0;
+    {
+        const uint32_t i0 = min(2 * (P - 1), np - 1), i1 = min(2 * (P - 1) + 1, np - 1);
+        nid0 = ids[i0];
+        nid1 = ids[i1];
+    }
+    #pragma unroll 1
+    for (uint32_t pi = 0; pi < npairs; ++pi) {
+        if (pi + P - 1 <= npairs) wait_vmcnt_const<(P - 3) * C::PER_PAIR>();   // pair pi + 1 has landed
+        else if (pi + 1 < npairs) wait_vmcnt((npairs - pi - 2) * C::PER_PAIR);
+        block_barrier();
+        if (pi + P - 1 < npairs)
+            dma_pair_pages<D>(a, __builtin_amdgcn_readfirstlane(nid0), __builtin_amdgcn_readfirstlane(nid1), src,
+                              ring_lds, ps == 0 ? P - 1 : ps - 1, wave);
+        {
+            const uint32_t i0 = min(2 * (pi + P), np - 1), i1 = min(2 * (pi + P) + 1, np - 1);
+            nid0 = ids[i0];
+            nid1 = ids[i1];
         }
-        if (!moved) break;
         if constexpr (NRT > 0) {
-            // Slow path for pair pi: move each row's max to the pair's max
-            // where it passed the old one by kLazyDma, rescale that row's
-            // accumulators, then finish the pair.
+            const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
+            const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
+            const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
+            // A row's reference max moves only when a score passes it by
+            // kLazyDma (always on the item's first pair, where m is -inf).
+            bool need = false;
+            float lm[RT];
             #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
-                const float lm = dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);   // already masked
-                const float mx = rowgroup_max(lm);
-                const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
-                const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
-                m[rt] = mnew;
-                Lsum[rt] *= alpha;
-                #pragma unroll
-                for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
+                lm[rt] = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
+                                 : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
+                need |= lm[rt] > m[rt] + kLazyDma;
             }
+            if (__ballot(need)) {
+                #pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) {
+                    const float mx = rowgroup_max(lm[rt]);
+                    const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
+                    const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+                    m[rt] = mnew;
+                    Lsum[rt] *= alpha;
+                    #pragma unroll
+                    for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
+                }
+            }
+            if constexpr (TAIL) {
+                if (partial) {
+                    dma_v_operands<D>(ring_lds + ps * 2 * C::PAGE, lo, vop);
+                    #pragma unroll
+                    for (int e = 0; e < D / 16; ++e) {
+                        mask_v_tr(vop[e], 0, g, n0);
+                        mask_v_tr(vop[e], 2, g, n1);
+                    }
+                }
+            }
+            // Branch-free from here, so the scheduler sees one region: LDS
+            // reads first, then the score MFMAs of pair pi + 1 interleaved
+            // with the softmax of pair pi, then the PV MFMAs.  On the last
+            // pair the K reads and score MFMAs run on a stale slot and
+            // their result is never used.
+            __builtin_amdgcn_sched_barrier(0);
+            if (!(TAIL && partial)) dma_v_operands<D>(ring_lds + ps * 2 * C::PAGE, lo, vop);
+            u32x4 kop[2][KB];
+            dma_k_operands<D>(ring_lds + psn * 2 * C::PAGE, lo, kop);
+            __builtin_amdgcn_sched_barrier(0);
             u32x4 pB[RT];
             #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
-            dma_pv_regs<D, F16, NRT, TAIL>(vop, partial, n0, n1, g, pB, O);
+            dma_score_mma<D, F16, NRT>(kop, qB, sc);
+            #pragma unroll
+            for (int k = 0; k < NRT * 2 * KB; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int e = 0; e < D / 16; ++e) {
+                #pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
+            }
         }
-        ps = ps + 1 == P ? 0 : ps + 1;
-        ++pi;
+        ps = psn;
+        psn = psn + 1 == P ? 0 : psn + 1;
     }
     // The last pair's wait was vmcnt(0): no ring load is outstanding.
 }
