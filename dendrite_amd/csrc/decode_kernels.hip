@@ -5,10 +5,12 @@
 //     rows, i.e. one sequence's GQA group of a private tail, or a few
 //     sequences of a small shared segment) over the item's pages, with the
 //     next page pair's loads in flight behind the current pair's math; or
-//   - one group item (<= 128 rows, a tree-shared prefix): every wave owns 32
-//     rows and all four consume the same page pairs, which the workgroup
-//     stages once into LDS (double-buffered, loads issued two pairs ahead),
-//     so a shared page is fetched once per 128 rows instead of once per wave.
+//   - one group item (<= 128 rows, a tree-shared prefix; 64 at head_dim 256
+//     and with FP8 KV): every wave owns up to 32 rows and all four consume
+//     the same page pairs, which the workgroup stages once into LDS (16-bit
+//     KV: direct global->LDS loads into a ring of page pairs; FP8 / MXFP8:
+//     through registers, double-buffered), so a shared page is fetched once
+//     per 128 rows instead of once per wave.
 // Each wave keeps an online softmax for its rows and writes one partial
 // state per row.  ReferenceBackend::decode (crates/dendrite-core/src/
 // attention/backend.rs:206-265) computes softmax(q K^T * scale) V over the
@@ -26,6 +28,8 @@
 //   (V^T) holds, for d-block e, V[token][c*EPL + e] for the lane's 8 tokens,
 //   built by byte permutes from 16-byte row loads (EPL = head_dim / 16).
 //   Lane (g, c) ends up holding O[row c][4g*EPL .. 4g*EPL + 4*EPL).
+//   (The LDS path of group items builds V^T with transposing LDS reads
+//   instead, and its lanes hold O[row c][16e + 4g + i]; see there.)
 // FP8 E4M3 pages are converted to bf16 in registers (exact: E4M3 is a subset
 // of bf16); the per-(page, head) fp32 scale multiplies the scores (K) and the
 // probabilities (V), which equals dequantising every element.  MXFP8 pages
