@@ -144,9 +144,15 @@ def main():
     plans, qs, outs, lpls = [], [], [], []
     for w in ws_list:
         ids = w.page_ids()
-        data, scales = w.make_pages(ids)
-        pool.write_pages(ids, data, scales)
-        del data, scales
+        # Synthesised and uploaded in chunks: bounded host memory, and a
+        # progress line per chunk for the multi-GB configs (C4, C5).
+        chunk = 8192
+        for c0 in range(0, len(ids), chunk):
+            data, scales = w.make_pages(ids[c0:c0 + chunk])
+            pool.write_pages(ids[c0:c0 + chunk], data, scales)
+            del data, scales
+            if len(ids) > chunk:
+                log(f"[bench] pages {min(c0 + chunk, len(ids))}/{len(ids)} written")
         plan = DecodePlan(be, w.attention_config(), pool, w.indptr, w.indices, cascade=True,
                           shared_chunk_pages=args.shared_chunk,
                           private_chunk_pages=args.private_chunk, target_items=args.target_items)

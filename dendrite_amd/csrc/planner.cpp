@@ -182,6 +182,20 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         if (count_waves(group_chunk, wave_chunk) >= target) break;
         if (group_chunk > 8) group_chunk /= 2;
     }
+    // With default options and work to spare (four times the target), longer
+    // chunks: fewer partial states for the merge to read and fewer item
+    // starts.  Private chunks grow first (to 32 pages), then shared ones (to
+    // kGroupMaxPages).  Measured on MI355X: C4 private 8 -> 32 pages took the
+    // step from 322 to 250 us; C5 shared 32 -> 256 pages cut its merge from
+    // 113 to 19 us.
+    if (!in.shared_chunk_pages && !in.private_chunk_pages && !in.target_items) {
+        constexpr uint32_t kMaxWaveChunk = 32;
+        while (count_waves(group_chunk, wave_chunk) >= 4ull * target &&
+               (wave_chunk < kMaxWaveChunk || group_chunk < uint32_t(kGroupMaxPages))) {
+            if (wave_chunk < kMaxWaveChunk) wave_chunk *= 2;
+            else group_chunk = std::min<uint32_t>(2 * group_chunk, kGroupMaxPages);
+        }
+    }
 
     // 4. Partial-state slots: one per (segment chunk, sequence), contiguous
     //    per sequence.
