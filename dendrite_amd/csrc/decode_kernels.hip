@@ -49,6 +49,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t KVF_F16 = 0, KVF_BF16 = 1, KVF_F32 = 2, KVF_FP8 = 3, KVF_MX = 4;
 constexpr float kNegInf = -__builtin_inff();
@@ -1117,6 +1118,78 @@ __device__ __forceinline__ void dma_pv_regs(u32x4 (&vop)[D / 16], bool partial, 
     }
 }
 
+// One iteration of the pair loop after its barrier: the lazy-max check of
+// pair pi (scores already in sc) and its rare rescale, then the LDS reads
+// (V of pair pi from slot vslot, K of pair pi + 1 from slot kslot), the score
+// MFMAs of pair pi + 1 interleaved with the softmax of pair pi, and the PV
+// MFMAs.  On the last pair kslot is stale and the scores it gives are unused.
+template <int D, bool F16, int NRT, bool TAIL>
+__device__ __forceinline__ void dma_step(uint32_t vslot, uint32_t kslot, int n0, int n1, const LdsOffsets& lo,
+                                         const u32x4 (&qB)[DmaCfg<D>::RT][D / 32], f4 (&sc)[DmaCfg<D>::RT][2],
+                                         u32x4 (&vop)[D / 16], float (&m)[DmaCfg<D>::RT],
+                                         f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], int g,
+                                         float f) {
+    constexpr int RT = DmaCfg<D>::RT, KB = D / 32;
+    const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
+    // A row's reference max moves only when a score passes it by
+    // kLazyDma (always on the item's first pair, where m is -inf).
+    bool need = false;
+    float lm[RT];
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        lm[rt] = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
+                         : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
+        need |= lm[rt] > m[rt] + kLazyDma;
+    }
+    if (__ballot(need)) {
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const float mx = rowgroup_max(lm[rt]);
+            const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
+            const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
+            m[rt] = mnew;
+            Lsum[rt] *= alpha;
+            #pragma unroll
+            for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
+        }
+    }
+    if constexpr (TAIL) {
+        if (partial) {
+            dma_v_operands<D>(vslot, lo, vop);
+            #pragma unroll
+            for (int e = 0; e < D / 16; ++e) {
+                mask_v_tr(vop[e], 0, g, n0);
+                mask_v_tr(vop[e], 2, g, n1);
+            }
+        }
+    }
+    // Branch-free from here, so the scheduler sees one region: LDS
+    // reads first, then the score MFMAs of pair pi + 1 interleaved
+    // with the softmax of pair pi, then the PV MFMAs.  On the last
+    // pair the K reads and score MFMAs run on a stale slot and
+    // their result is never used.
+    __builtin_amdgcn_sched_barrier(0);
+    if (!(TAIL && partial)) dma_v_operands<D>(vslot, lo, vop);
+    u32x4 kop[2][KB];
+    dma_k_operands<D>(kslot, lo, kop);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 pB[RT];
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
+    dma_score_mma<D, F16, NRT>(kop, qB, sc);
+    #pragma unroll
+    for (int k = 0; k < NRT * 2 * KB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+    for (int e = 0; e < D / 16; ++e) {
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
+    }
+}
+
 // Where the rows of a wave's tiles come from and go to: the byte offset of
 // the query row in q and the partial-state row, read once per item.  Rows
 // past the item's last are given its last row (their query is zeroed and
@@ -1238,64 +1311,8 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
         if constexpr (NRT > 0) {
             const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
             const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
-            const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
-            // A row's reference max moves only when a score passes it by
-            // kLazyDma (always on the item's first pair, where m is -inf).
-            bool need = false;
-            float lm[RT];
-            #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) {
-                lm[rt] = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
-                                 : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
-                need |= lm[rt] > m[rt] + kLazyDma;
-            }
-            if (__ballot(need)) {
-                #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) {
-                    const float mx = rowgroup_max(lm[rt]);
-                    const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
-                    const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
-                    m[rt] = mnew;
-                    Lsum[rt] *= alpha;
-                    #pragma unroll
-                    for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
-                }
-            }
-            if constexpr (TAIL) {
-                if (partial) {
-                    dma_v_operands<D>(ring_lds + ps * 2 * C::PAGE, lo, vop);
-                    #pragma unroll
-                    for (int e = 0; e < D / 16; ++e) {
-                        mask_v_tr(vop[e], 0, g, n0);
-                        mask_v_tr(vop[e], 2, g, n1);
-                    }
-                }
-            }
-            // Branch-free from here, so the scheduler sees one region: LDS
-            // reads first, then the score MFMAs of pair pi + 1 interleaved
-            // with the softmax of pair pi, then the PV MFMAs.  On the last
-            // pair the K reads and score MFMAs run on a stale slot and
-            // their result is never used.
-            __builtin_amdgcn_sched_barrier(0);
-            if (!(TAIL && partial)) dma_v_operands<D>(ring_lds + ps * 2 * C::PAGE, lo, vop);
-            u32x4 kop[2][KB];
-            dma_k_operands<D>(ring_lds + psn * 2 * C::PAGE, lo, kop);
-            __builtin_amdgcn_sched_barrier(0);
-            u32x4 pB[RT];
-            #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
-            dma_score_mma<D, F16, NRT>(kop, qB, sc);
-            #pragma unroll
-            for (int k = 0; k < NRT * 2 * KB; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            #pragma unroll
-            for (int e = 0; e < D / 16; ++e) {
-                #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
-            }
+            dma_step<D, F16, NRT, TAIL>(ring_lds + ps * 2 * C::PAGE, ring_lds + psn * 2 * C::PAGE, n0, n1, lo, qB,
+                                        sc, vop, m, Lsum, O, g, f);
         }
         ps = psn;
         psn = psn + 1 == P ? 0 : psn + 1;
@@ -1396,6 +1413,285 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
     else dma_group_run<D, F16, 0>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
 }
 
+// ------------------------------------------- group items, FP8 / MXFP8 KV
+// Raw E4M3 pages and their scales reach LDS by direct loads into a ring of
+// NPR raw pairs.  Each raw pair is then converted by the whole workgroup
+// into a bf16 pair slot laid out as the 16-bit path's (swizzled rows), and
+// the 16-bit pair loop's compute (dma_step) runs on those slots.  MXFP8
+// elements take their E8M0 group scale in the exact power-of-two conversion;
+// E4M3 with a block scale is converted exactly to f32, multiplied by the
+// scale and rounded to bf16: K and V dequantised to the query dtype, as
+// ReferenceBackend computes them.  Per iteration pi: wait for raw pair
+// pi + 1, barrier, refill the raw slot of pair pi - 1 (converted two
+// iterations ago), convert raw pair pi + 1 into bf16 slot (pi + 1) & 1,
+// barrier, compute.  Head_dim 128 and 256 (64 keeps the register path).
+template <int D>
+struct Dma8Cfg {
+    using C16 = DmaCfg<D>;
+    static constexpr int RAW_PLANE = kPageSize * D;              // E4M3 bytes of one plane
+    static constexpr int RAW_PAGE = 2 * RAW_PLANE;
+    static constexpr int RAW_PAIR = 2 * RAW_PAGE;
+    static constexpr int NPR = 4;                                // raw ring pairs
+    static constexpr int RDPP = RAW_PAGE / (kWaves * 1024);      // wave loads per thread per raw page
+    static constexpr int PER_PAIR = 2 * RDPP + 1;                // + the pair's scale load
+    static constexpr int SCALES = 1024;                          // LDS bytes of one raw pair's scales
+    static constexpr int SREC = kPageSize * (D / 32);            // MXFP8 scale bytes of one plane
+    static constexpr int NCH = 4 * SREC / 16;                    // 16-byte chunks of a pair's MX scales
+    static constexpr int BF_PAIR = 2 * C16::PAGE;                // bf16 pair slot
+    static constexpr int RAW_BYTES = NPR * (RAW_PAIR + SCALES);
+    static constexpr int LDS = RAW_BYTES + 2 * BF_PAIR;
+    static constexpr int CONV = RAW_PAIR / (kWaves * 64 * 32);   // 32-element runs per thread per pair
+    static_assert(RDPP >= 1 && RDPP <= 4 && CONV >= 1, "head_dim 128 or 256");
+    static_assert(C16::QBYTES <= 2 * BF_PAIR, "query rows fit the bf16 slots");
+    static_assert(4 * SREC <= SCALES && NCH <= 64, "scale slot");
+    static_assert(NPR * PER_PAIR <= 63, "vmcnt range");
+};
+
+// One wave load of 64 x 4 bytes from gbase + voff (per lane) to lds + 4 * lane.
+__device__ __forceinline__ void dma_x1(uint32_t lds, const void* gbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n), n <= 63, from a run-time value.
+__device__ __forceinline__ void wait_vmcnt_any(uint32_t n) {
+#define DH_VMCNT_CASE(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+    switch (n) {
+        DH_VMCNT_CASE(0) DH_VMCNT_CASE(1) DH_VMCNT_CASE(2) DH_VMCNT_CASE(3) DH_VMCNT_CASE(4)
+        DH_VMCNT_CASE(5) DH_VMCNT_CASE(6) DH_VMCNT_CASE(7) DH_VMCNT_CASE(8) DH_VMCNT_CASE(9)
+        DH_VMCNT_CASE(10) DH_VMCNT_CASE(11) DH_VMCNT_CASE(12) DH_VMCNT_CASE(13) DH_VMCNT_CASE(14)
+        DH_VMCNT_CASE(15) DH_VMCNT_CASE(16) DH_VMCNT_CASE(17) DH_VMCNT_CASE(18) DH_VMCNT_CASE(19)
+        DH_VMCNT_CASE(20) DH_VMCNT_CASE(21) DH_VMCNT_CASE(22) DH_VMCNT_CASE(23) DH_VMCNT_CASE(24)
+        DH_VMCNT_CASE(25) DH_VMCNT_CASE(26) DH_VMCNT_CASE(27) DH_VMCNT_CASE(28) DH_VMCNT_CASE(29)
+        DH_VMCNT_CASE(30) DH_VMCNT_CASE(31) DH_VMCNT_CASE(32) DH_VMCNT_CASE(33) DH_VMCNT_CASE(34)
+        DH_VMCNT_CASE(35) DH_VMCNT_CASE(36) DH_VMCNT_CASE(37) DH_VMCNT_CASE(38) DH_VMCNT_CASE(39)
+        DH_VMCNT_CASE(40) DH_VMCNT_CASE(41) DH_VMCNT_CASE(42) DH_VMCNT_CASE(43) DH_VMCNT_CASE(44)
+        DH_VMCNT_CASE(45) DH_VMCNT_CASE(46) DH_VMCNT_CASE(47) DH_VMCNT_CASE(48)
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+#undef DH_VMCNT_CASE
+}
+
+// Source offsets (per lane) of one raw pair's loads.
+template <int D>
+struct Dma8Src {
+    uint32_t loff[Dma8Cfg<D>::RDPP];    // inside a raw page, this wave's share
+    uint64_t page_stride;
+    uint32_t s_rel;                     // scale load: offset inside the (page, plane) record
+    uint32_t s_plane;                   // scale load: plane of this lane's chunk
+    bool s_page1;                       // scale load: this lane's chunk belongs to the pair's second page
+};
+
+template <int D, uint32_t KVF>
+__device__ __forceinline__ Dma8Src<D> dma8_src(const AttendArgs& a, const Item& it, int wave, int lane) {
+    using C8 = Dma8Cfg<D>;
+    Dma8Src<D> s;
+    s.page_stride = uint64_t(2) * a.hkv * C8::RAW_PLANE;
+    #pragma unroll
+    for (int u = 0; u < C8::RDPP; ++u) {
+        const int b = (wave * C8::RDPP + u) * 1024 + 16 * lane;
+        const int plane = b / C8::RAW_PLANE, rem = b - plane * C8::RAW_PLANE;
+        s.loff[u] = uint32_t((plane * a.hkv + it.kv_head) * C8::RAW_PLANE + rem);
+    }
+    if constexpr (KVF == KVF_MX) {
+        const int k = lane % C8::NCH, pp = k / (C8::SREC / 16);
+        s.s_page1 = (pp >> 1) != 0;
+        s.s_plane = uint32_t(pp & 1);
+        s.s_rel = uint32_t((k % (C8::SREC / 16)) * 16);
+    } else {
+        const int e = lane & 3;
+        s.s_page1 = (e >> 1) != 0;
+        s.s_plane = uint32_t(e & 1);
+        s.s_rel = 0;
+    }
+    return s;
+}
+
+// Issues this wave's loads of pages pg0, pg1 (and their scales) into raw slot rs.
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void dma8_pair(const AttendArgs& a, const Item& it, uint32_t pg0, uint32_t pg1,
+                                          const Dma8Src<D>& src, uint32_t raw_lds, uint32_t rs, int wave) {
+    using C8 = Dma8Cfg<D>;
+    const uint32_t slot = raw_lds + rs * (C8::RAW_PAIR + C8::SCALES);
+    #pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint8_t* base = a.kv + uint64_t(q == 0 ? pg0 : pg1) * src.page_stride;
+        const uint32_t dst = slot + q * C8::RAW_PAGE + wave * C8::RDPP * 1024;
+        #pragma unroll
+        for (int u = 0; u < C8::RDPP; ++u) dma_x4(dst + u * 1024, base, src.loff[u]);
+    }
+    const uint32_t pg = src.s_page1 ? pg1 : pg0;
+    const uint32_t rec = (pg * 2 + src.s_plane) * a.hkv + it.kv_head;
+    if constexpr (KVF == KVF_MX)
+        dma_x4(slot + C8::RAW_PAIR, a.scales, rec * uint32_t(C8::SREC) + src.s_rel);
+    else
+        dma_x1(slot + C8::RAW_PAIR, a.scales, rec * 4u);
+}
+
+// Converts raw slot rs into bf16 slot bs (the whole workgroup; tid < 256).
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_t bs, int tid) {
+    using C8 = Dma8Cfg<D>;
+    using C = DmaCfg<D>;
+    const uint8_t* raw = ring + rs * (C8::RAW_PAIR + C8::SCALES);
+    const uint8_t* scl = raw + C8::RAW_PAIR;
+    uint8_t* bf = ring + C8::RAW_BYTES + bs * C8::BF_PAIR;
+    #pragma unroll
+    for (int k = 0; k < C8::CONV; ++k) {
+        const int o = 32 * (tid + kWaves * 64 * k);
+        const int page = o / C8::RAW_PAGE, po = o - page * C8::RAW_PAGE;
+        const int plane = po / C8::RAW_PLANE, pr = po - plane * C8::RAW_PLANE;
+        const int row = pr / D, col0 = pr - row * D;
+        const u32x4 w0 = *reinterpret_cast<const u32x4*>(raw + o);
+        const u32x4 w1 = *reinterpret_cast<const u32x4*>(raw + o + 16);
+        const uint32_t wd[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+        uint32_t out[16];
+        if constexpr (KVF == KVF_MX) {
+            const float sc = e8m0_to_float(scl[(page * 2 + plane) * C8::SREC + row * (D / 32) + col0 / 32]);
+            #pragma unroll
+            for (int w = 0; w < 8; ++w) e4m3x4_to_bf16(wd[w], sc, out[2 * w], out[2 * w + 1]);
+        } else {
+            const float sc = *reinterpret_cast<const float*>(scl + 4 * (page * 2 + plane));
+            #pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], false);
+                const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], true);
+                out[2 * w] = pack2(lo[0] * sc, lo[1] * sc, false);
+                out[2 * w + 1] = pack2(hi[0] * sc, hi[1] * sc, false);
+            }
+        }
+        uint8_t* rowp = bf + page * C::PAGE + plane * C::PLANE + row * C::RB;
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int pos = (col0 / 8 + j) ^ chunk_swz<D>(row);
+            *reinterpret_cast<u32x4*>(rowp + pos * 16) = u32x4{out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]};
+        }
+    }
+}
+
+template <int D, uint32_t KVF, int NRT, bool TAIL>
+__device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                                uint8_t* ring, int tid, int wave, int g, int c,
+                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
+                                                u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
+                                                float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
+                                                f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+    using C = DmaCfg<D>;
+    using C8 = Dma8Cfg<D>;
+    constexpr uint32_t P = C8::NPR;
+    constexpr int RT = C::RT, KB = D / 32;
+    const uint32_t np = it.npages;
+    const uint32_t npairs = (np + 1) >> 1;
+    const int lane = tid & 63;
+    const Dma8Src<D> src = dma8_src<D, KVF>(a, it, wave, lane);
+    const LdsOffsets lo = lds_offsets<D>(g, c);
+    const uint32_t raw_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
+    const uint32_t bf_lds = raw_lds + C8::RAW_BYTES;
+    auto page_id = [&](uint32_t i) { return __builtin_amdgcn_readfirstlane(ids[i < np ? i : np - 1]); };
+    // Every compiler-issued load (row targets, page ids) has landed before
+    // the ring loads start, so no compiler-inserted wait drains the ring.
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    compiler_fence();
+    const uint32_t q_lds = bf_lds + wave * (RT * KB * 1024);
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        #pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+            dma_x4(q_lds + (rt * KB + kb) * 1024, static_cast<const uint8_t*>(a.q), rtg.qoff[rt] + kb * 64 + 16 * g);
+    }
+    const uint32_t pro = min(P - 1, npairs);
+    #pragma unroll 1
+    for (uint32_t q = 0; q < pro; ++q) dma8_pair<D, KVF>(a, it, page_id(2 * q), page_id(2 * q + 1), src, raw_lds, q, wave);
+    wait_vmcnt_any(pro * C8::PER_PAIR);   // loads land in issue order: the query rows are in
+    if constexpr (NRT > 0) {
+        const uint8_t* qw = ring + C8::RAW_BYTES + wave * (RT * KB * 1024) + 16 * lane;
+        #pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const bool valid = uint32_t(rt * kWaves + wave) * kTileRows + c < it.nrows;
+            #pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024);
+                qB[rt][kb] = valid ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+    wait_vmcnt_any((pro - 1) * C8::PER_PAIR);   // raw pair 0 has landed
+    block_barrier();                             // query rows read; raw pair 0 visible
+    dma8_convert<D, KVF>(ring, 0, 0, tid);
+    block_barrier();
+    const float f = a.scale_log2;
+    f4 sc[RT][2];
+    u32x4 vop[D / 16];
+    if constexpr (NRT > 0) dma_scores<D, false, NRT>(bf_lds, lo, qB, sc);
+    uint32_t ps = 0, psn = 1;   // raw slots of pairs pi, pi + 1
+    uint32_t nid0 = page_id(2 * (P - 1)), nid1 = page_id(2 * (P - 1) + 1);
+    #pragma unroll 1
+    for (uint32_t pi = 0; pi < npairs; ++pi) {
+        if (pi + 1 < npairs) wait_vmcnt_any((min(pi + P - 1, npairs) - pi - 2) * C8::PER_PAIR);   // raw pair pi + 1
+        block_barrier();
+        if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
+        nid0 = page_id(2 * (pi + P));
+        nid1 = page_id(2 * (pi + P) + 1);
+        if (pi + 1 < npairs) dma8_convert<D, KVF>(ring, psn, (pi + 1) & 1, tid);
+        block_barrier();
+        if constexpr (NRT > 0) {
+            const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
+            const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
+            dma_step<D, false, NRT, TAIL>(bf_lds + (pi & 1) * C8::BF_PAIR, bf_lds + ((pi + 1) & 1) * C8::BF_PAIR,
+                                          n0, n1, lo, qB, sc, vop, m, Lsum, O, g, f);
+        }
+        ps = psn;
+        psn = psn + 1 == P ? 0 : psn + 1;
+    }
+    // The last wait was vmcnt(0): no ring load is outstanding.
+}
+
+template <int D, uint32_t KVF, int NRT>
+__device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
+                                               uint8_t* ring, int tid, int wave, int g, int c,
+                                               const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
+    using C = DmaCfg<D>;
+    constexpr int RT = C::RT, EPL = D / 16, KB = D / 32;
+    u32x4 qB[RT][KB];
+    float m[RT];
+    f4 L[RT];
+    f4 O[RT][EPL];
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = kNegInf;
+        L[rt] = f4{0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (it.flags & kItemTail)
+        dma8_group_loop<D, KVF, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
+    else
+        dma8_group_loop<D, KVF, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
+    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, m, L, O, g, c);
+}
+
+template <int D, uint32_t KVF>
+__device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item& item, int tid, int wave, int g,
+                                                int c) {
+    using C = DmaCfg<D>;
+    using C8 = Dma8Cfg<D>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[C8::LDS];
+    __shared__ uint32_t ids[kGroupMaxPages];
+    const Item it = uniform_item(item);
+    RowTargets<C::RT> rtg;
+    dma_row_targets<D, C::RT>(a, it, wave, c, rtg);
+    const int last_len = item_last_len(a, it);
+    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) ids[i] = a.pages[it.page_off + i];
+    __syncthreads();
+    const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
+    const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
+    if (nrt >= 2) dma8_group_run<D, KVF, C::RT>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 1) dma8_group_run<D, KVF, 1>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else dma8_group_run<D, KVF, 0>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+}
+
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
 template <int D, uint32_t KVF, bool F16>
@@ -1406,7 +1702,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (blockIdx.x < a.n_group_items) {
         const Item it = a.items[blockIdx.x];
-        if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
+        if constexpr ((KVF == KVF_FP8 || KVF == KVF_MX) && D == 64) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
+        else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF>(a, it, tid, wave, g, c);
         else group_item_dma<D, F16>(a, it, tid, wave, g, c);
     } else {
         const uint32_t idx = wave_item_index(a, wave);

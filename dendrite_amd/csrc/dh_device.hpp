@@ -25,14 +25,15 @@ constexpr int kWaves = 4;           // wave64s per workgroup
 constexpr int kTileRows = 16;       // query rows of one MFMA tile
 constexpr int kWaveRows = 16;       // rows of a wave item: one tile, one wave
 constexpr int kGroupMaxPages = 256; // pages of one group item (LDS page-id list)
-// Row tiles per wave of a group item: 16-bit KV pages (staged by direct
-// global->LDS loads) use two (one at head_dim 256, for registers), FP8 /
-// MXFP8 pages (staged through registers) one.  A group item has
+// Row tiles per wave of a group item: pages staged by direct global->LDS
+// loads (16-bit KV; FP8 / MXFP8 at head_dim 128 and 256, converted to bf16
+// in LDS) use two (one at head_dim 256, for registers); FP8 / MXFP8 pages at
+// head_dim 64 (staged through registers) one.  A group item has
 // kWaves * tiles * 16 rows.
 constexpr int kGroupTiles8 = 1;
 DH_HOST_DEVICE constexpr int group_tiles16(int head_dim) { return head_dim == 256 ? 1 : 2; }
 DH_HOST_DEVICE constexpr int group_rows(bool fp8_kv, int head_dim) {
-    return kWaves * (fp8_kv ? kGroupTiles8 : group_tiles16(head_dim)) * kTileRows;
+    return kWaves * ((fp8_kv && head_dim == 64) ? kGroupTiles8 : group_tiles16(head_dim)) * kTileRows;
 }
 
 // One attention work item (32 bytes): a run of pages of one segment chunk,
