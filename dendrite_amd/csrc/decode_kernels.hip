@@ -512,66 +512,87 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
     for (int e = 0; e < EPL; ++e) O[0][e] = f4{0.f, 0.f, 0.f, 0.f};
 
     const int last_len = item_last_len(a, it);
-    const uint32_t* pages = a.pages + it.page_off;
     const uint32_t head = it.kv_head;
     const uint32_t np = it.npages;
     const float* bsc = reinterpret_cast<const float*>(a.scales);
+    // The item's page ids in registers (lane l holds ids l, l + 64, ...), so
+    // a refill needs no memory round trip of its own: a load issued just
+    // before a refill would be the newest outstanding one, and waiting for it
+    // would also drain the page loads in flight.
+    const int lane = 16 * g + c;
+    uint32_t idv[kWaveIdRegs];
+    #pragma unroll
+    for (int k = 0; k < kWaveIdRegs; ++k) {
+        const uint32_t i = uint32_t(lane + 64 * k);
+        idv[k] = i < np ? a.pages[it.page_off + i] : 0u;
+    }
+    auto page_id = [&](uint32_t i) -> uint32_t {
+        i = i < np ? i : np - 1;
+        uint32_t r = 0;
+        #pragma unroll
+        for (int k = 0; k < kWaveIdRegs; ++k)
+            if ((i >> 6) == uint32_t(k)) r = __builtin_amdgcn_readlane(idv[k], int(i & 63));
+        return r;
+    };
 
-    PageRaw<D, KVF> pr[2];
-    float ks[2] = {1.f, 1.f}, vs[2] = {1.f, 1.f};
-    {
-        uint32_t pg[2];
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) pg[p] = pages[uint32_t(p) < np ? p : np - 1];
+    // DEPTH page pairs in flight: buffer p % DEPTH holds pair p; once pair
+    // p's K (then V) has been consumed, its K (V) registers take pair
+    // p + DEPTH's.  Two for E4M3 pages at head_dim <= 128 (a pair is 32
+    // registers); one where a second pair would not fit beside the math.
+    constexpr int DEPTH = (KVF == KVF_FP8 && D <= 128) ? 2 : 1;
+    PageRaw<D, KVF> pr[DEPTH][2];
+    float ks[DEPTH][2], vs[DEPTH][2];
+    #pragma unroll
+    for (int d = 0; d < DEPTH; ++d) ks[d][0] = ks[d][1] = vs[d][0] = vs[d][1] = 1.f;
+    auto load_pair = [&](int buf, uint32_t pair, bool kpart) {
         #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            load_page_k<D, KVF>(pr[p], a, pg[p], head, g, c);
-            if constexpr (BLOCK_SCALE) ks[p] = bsc[(uint64_t(pg[p]) * 2 + 0) * a.hkv + head];
+            const uint32_t pg = page_id(2 * pair + p);
+            if (kpart) {
+                load_page_k<D, KVF>(pr[buf][p], a, pg, head, g, c);
+                if constexpr (BLOCK_SCALE) ks[buf][p] = bsc[(uint64_t(pg) * 2 + 0) * a.hkv + head];
+            } else {
+                load_page_v<D, KVF>(pr[buf][p], a, pg, head, g, c);
+                if constexpr (BLOCK_SCALE) vs[buf][p] = bsc[(uint64_t(pg) * 2 + 1) * a.hkv + head];
+            }
         }
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            load_page_v<D, KVF>(pr[p], a, pg[p], head, g, c);
-            if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pg[p]) * 2 + 1) * a.hkv + head];
+    };
+    const uint32_t npairs = (np + 1) >> 1;
+    #pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+        if (uint32_t(d) < npairs) {
+            load_pair(d, d, true);
+            load_pair(d, d, false);
         }
     }
-    const uint32_t npairs = (np + 1) >> 1;
-    for (uint32_t pi = 0; pi < npairs; ++pi) {
+    auto step = [&](int buf, uint32_t pi) {
         const uint32_t i0 = 2 * pi;
         const int n0 = page_tokens(it, i0, last_len);
         const int n1 = page_tokens(it, i0 + 1, last_len);
-        uint32_t pgn[2];
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t i = i0 + 2 + p;
-            pgn[p] = pages[i < np ? i : np - 1];
-        }
         uint32_t kop[2][KB][4];
-        k_operand<D, KVF>(pr[0], kop[0]);
-        k_operand<D, KVF>(pr[1], kop[1]);
-        f4 s[1][2];
-        pair_scores<D, F16, 1, 1>(kop, qB, s);
-        const float f0 = a.scale_log2 * ks[0], f1 = a.scale_log2 * ks[1];
-        const float v0s = vs[0], v1s = vs[1];
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            load_page_k<D, KVF>(pr[p], a, pgn[p], head, g, c);
-            if constexpr (BLOCK_SCALE) ks[p] = bsc[(uint64_t(pgn[p]) * 2 + 0) * a.hkv + head];
-        }
+        k_operand<D, KVF>(pr[buf][0], kop[0]);
+        k_operand<D, KVF>(pr[buf][1], kop[1]);
+        f4 sc[1][2];
+        pair_scores<D, F16, 1, 1>(kop, qB, sc);
+        const float f0 = a.scale_log2 * ks[buf][0], f1 = a.scale_log2 * ks[buf][1];
+        const float v0s = vs[buf][0], v1s = vs[buf][1];
+        const bool refill = pi + DEPTH < npairs;
+        if (refill) load_pair(buf, pi + DEPTH, true);
         uint32_t vop[2][4][D / 32];
         const bool full = (n0 == kPageSize) && (n1 == kPageSize);
         if (full) {
-            v_operand<D, KVF>(pr[0], g, kPageSize, vop[0]);
-            v_operand<D, KVF>(pr[1], g, kPageSize, vop[1]);
+            v_operand<D, KVF>(pr[buf][0], g, kPageSize, vop[0]);
+            v_operand<D, KVF>(pr[buf][1], g, kPageSize, vop[1]);
         } else {
-            v_operand<D, KVF>(pr[0], g, n0, vop[0]);
-            v_operand<D, KVF>(pr[1], g, n1, vop[1]);
+            v_operand<D, KVF>(pr[buf][0], g, n0, vop[0]);
+            v_operand<D, KVF>(pr[buf][1], g, n1, vop[1]);
         }
-        pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(s, vop, n0, n1, f0, f1, v0s, v1s, m, L, O, g);
-        #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            load_page_v<D, KVF>(pr[p], a, pgn[p], head, g, c);
-            if constexpr (BLOCK_SCALE) vs[p] = bsc[(uint64_t(pgn[p]) * 2 + 1) * a.hkv + head];
-        }
+        pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(sc, vop, n0, n1, f0, f1, v0s, v1s, m, L, O, g);
+        if (refill) load_pair(buf, pi + DEPTH, false);
+    };
+    for (uint32_t pi = 0; pi < npairs; pi += DEPTH) {
+        step(0, pi);
+        if (DEPTH == 2 && pi + 1 < npairs) step(DEPTH - 1, pi + 1);
     }
     const float lr[1] = {L[0][0]};
     write_wave_partial<D, 1, true, false>(a, it, 0, 1, dst, m, lr, O, g, c);

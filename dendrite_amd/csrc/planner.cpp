@@ -162,7 +162,9 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     };
     uint32_t group_chunk = std::min<uint32_t>(in.shared_chunk_pages ? in.shared_chunk_pages : 32,
                                               kGroupMaxPages);
-    uint32_t wave_chunk = in.private_chunk_pages ? in.private_chunk_pages : 8;
+    // Wave items keep their page ids in registers (kWaveIdRegs x 64 at most).
+    uint32_t wave_chunk = std::min<uint32_t>(in.private_chunk_pages ? in.private_chunk_pages : 8,
+                                             uint32_t(kWaveIdRegs) * 64);
     const uint32_t target = in.target_items ? in.target_items : 1536;   // waves
     auto count_waves = [&](uint32_t gc, uint32_t wc) {
         uint64_t n = 0;
