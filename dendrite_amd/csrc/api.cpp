@@ -305,6 +305,19 @@ uint32_t dh_pool_num_pages(const dh_pool* p) { return p ? p->num_pages : 0; }
 void* dh_pool_data(dh_pool* p) { return p ? p->data : nullptr; }
 void* dh_pool_scales(dh_pool* p) { return p ? p->scales : nullptr; }
 
+// FP8 E4M3 block scales must be finite and positive: the kernels order a
+// page's scaled scores by its raw ones, and a masked -inf times 0 is NaN.
+// The quantiser never makes another (amax / 448, or 1 for an all-zero block).
+static bool fp8_scales_ok(const void* scales, uint64_t n) {
+    const uint8_t* b = static_cast<const uint8_t*>(scales);
+    for (uint64_t i = 0; i < n; ++i) {
+        float x;
+        memcpy(&x, b + 4 * i, 4);
+        if (!(x > 0.f) || isinf(x)) return false;
+    }
+    return true;
+}
+
 dh_status dh_pool_write_tokens(dh_pool* p, uint32_t page_id, uint32_t tok_offset, uint32_t n_tok,
                                const void* k, const void* v, const void* k_scale,
                                const void* v_scale, void* stream) {
@@ -315,6 +328,8 @@ dh_status dh_pool_write_tokens(dh_pool* p, uint32_t page_id, uint32_t tok_offset
                     tok_offset + n_tok, DH_PAGE_SIZE);
     if ((p->fmt == DH_KV_FP8_E4M3 || p->fmt == DH_KV_MXFP8) && (!k_scale || !v_scale))
         return fail(DH_EINVAL, "scales are required for this kv format");
+    if (p->fmt == DH_KV_FP8_E4M3 && (!fp8_scales_ok(k_scale, p->hkv) || !fp8_scales_ok(v_scale, p->hkv)))
+        return fail(DH_EINVAL, "FP8 block scales must be finite and positive");
     DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint64_t row = uint64_t(p->d) * p->eb;
@@ -354,6 +369,8 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
     for (uint32_t i = 0; i < n; ++i)
         if (ids[i] >= p->num_pages) return fail(DH_EINVAL, "page id %u outside the pool", ids[i]);
     if (n == 0) return DH_OK;
+    if (p->fmt == DH_KV_FP8_E4M3 && !fp8_scales_ok(scales, uint64_t(n) * p->scale_bytes / 4))
+        return fail(DH_EINVAL, "FP8 block scales must be finite and positive");
     DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint32_t batch = std::min<uint32_t>(n, std::max<uint64_t>(1, (256ull << 20) / p->page_bytes));
@@ -614,7 +631,11 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         a.hkv = c.num_kv_heads;
         a.r = c.num_heads / c.num_kv_heads;
         a.gqa_tiled = c.gqa_mapping == DH_GQA_TILED ? 1u : 0u;
-        a.scale_log2 = c.scale * 1.4426950408889634f;
+        // A negative scale goes into the query's sign; zero becomes 2^-60
+        // (scores * 2^-60 round to 0 in exp2, and a masked -inf stays -inf).
+        const float sl = c.scale * 1.4426950408889634f;
+        a.scale_log2 = std::max(fabsf(sl), 0x1p-60f);
+        a.q_sign = sl < 0.f ? (c.q_dtype == DH_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
         a.n_group_items = pl->n_group_items;
         a.n_wave_items = pl->n_wave_items;
         hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim, stream));

@@ -276,7 +276,11 @@ __device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, ui
             dst[rt] = slot * a.hq + qh;
             const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
             #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
+            for (int kb = 0; kb < KB; ++kb) {
+                load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) qB[rt][kb][i] ^= a.q_sign;
+            }
         } else {
             #pragma unroll
             for (int kb = 0; kb < KB; ++kb) qB[rt][kb][0] = qB[rt][kb][1] = qB[rt][kb][2] = qB[rt][kb][3] = 0u;
@@ -340,7 +344,8 @@ __device__ __forceinline__ void pair_softmax(const f4 (&s)[RT][2], int n0, int n
                 if (4 * g + i >= n1) x1[i] = kNegInf;
             }
         }
-        // Lane-local max over raw scores (the scale factors are positive).
+        // Lane-local max over raw scores: the scale factors are positive
+        // (scale_log2 > 0; FP8 block scales are checked on write).
         const float r0 = fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3]));
         const float r1 = fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]));
         const float lm = fmaxf(r0 * f0, r1 * f1);          // -inf * f stays -inf
@@ -945,10 +950,9 @@ __device__ __forceinline__ void block_barrier() {
 
 // Lane byte offsets inside a slot of the K operand read of k-block 0 and
 // the transposed V read of d-block 0.  The swizzle is an XOR on the chunk
-// index (bits 4.. of the offset) and slots start at multiples of 1 KiB, so
-// k-block kb is at (slot + k) ^ (kb << 6) and d-block e at (slot + v) ^ (e << 5):
-// chunk 4kb + g -> (4kb + g) ^ swz = 4 (kb ^ (swz >> 2)) + (g ^ (swz & 3)), and
-// chunk 2e + h likewise.  Two registers instead of one per block.
+// index (bits 4..7 of the offset): chunk 4kb + g -> (4kb + g) ^ swz =
+// 4 (kb ^ (swz >> 2)) + (g ^ (swz & 3)), so k-block kb is at k ^ (kb << 6)
+// and d-block e at v ^ (e << 5) (chunk 2e + h likewise).
 struct LdsOffsets {
     uint32_t k;
     uint32_t v;
@@ -966,6 +970,28 @@ __device__ __forceinline__ LdsOffsets lds_offsets(int g, int c) {
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
+// A lane's LDS read addresses for every k-block and d-block of a pair slot
+// at byte offset 0 from `base`.  Bases and slots are multiples of 1 KiB, so
+// the swizzle XOR (bits 4..7) and the slot offset commute: the block of a
+// slot at offset s is at k[kb] + s, and with s known at compile time the
+// read takes it as its immediate offset (no address arithmetic per pair).
+template <int D>
+struct LdsBases {
+    uint32_t k[D / 32];
+    uint32_t v[D / 16];
+};
+
+template <int D>
+__device__ __forceinline__ LdsBases<D> lds_bases(uint32_t base, int g, int c) {
+    const LdsOffsets o = lds_offsets<D>(g, c);
+    LdsBases<D> b;
+    #pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) b.k[kb] = base + (o.k ^ uint32_t(kb << 6));
+    #pragma unroll
+    for (int e = 0; e < D / 16; ++e) b.v[e] = base + (o.v ^ uint32_t(e << 5));
+    return b;
+}
+
 // Zeroes the V values of tokens 4g + j >= n (j = 0..3) in one page's half
 // (dwords w0, w0+1) of a transposed V operand.
 __device__ __forceinline__ void mask_v_tr(u32x4& v, int w0, int g, int n) {
@@ -978,16 +1004,26 @@ __device__ __forceinline__ void mask_v_tr(u32x4& v, int w0, int g, int n) {
 }
 
 // Softmax pieces of the DMA path.  Scores are in log2 units once multiplied
-// by f (scale * log2 e).  A row's reference max m moves only when a score
-// passes it by kLazyDma; in between, exp2(x - m) stays below 2^kLazyDma, far
-// inside f32 / bf16 range, so the accumulators never need rescaling on the
-// common path.  The rare move (always the item's first pair, where m starts
-// at -inf) runs on a slow path outside the pair loop.
+// by f = scale_log2 > 0 (a negative scale is folded into the query's sign).
+// A row's reference max m moves only when a score passes it by kLazyDma;
+// in between, exp2(x - m) stays below 2^kLazyDma, far inside f32 / bf16 /
+// f16-after-row-sum range, so the accumulators are not rescaled on the
+// common path.  The check compares the lane's raw score max with
+// thr = (m + kLazyDma) / f, kept per row, so the common path spends no
+// multiply on it.  The move (always on the item's first pair, where m and
+// thr start at -inf) runs on a slow path.
 constexpr float kLazyDma = 32.f;
 
-// Masks invalid tokens (PARTIAL) and returns the lane's max over the pair.
+template <int RT>
+struct RowMax {
+    float m[RT];     // reference max, log2 units
+    float thr[RT];   // raw score above which m must move
+};
+
+// Masks invalid tokens (PARTIAL) and returns the lane's raw score max over
+// the pair.
 template <int RT, bool PARTIAL>
-__device__ __forceinline__ float dma_lane_max(f4 (&s)[RT][2], int rt, int n0, int n1, int g, float f) {
+__device__ __forceinline__ float dma_lane_max(f4 (&s)[RT][2], int rt, int n0, int n1, int g) {
     f4& x0 = s[rt][0];
     f4& x1 = s[rt][1];
     if constexpr (PARTIAL) {
@@ -997,22 +1033,67 @@ __device__ __forceinline__ float dma_lane_max(f4 (&s)[RT][2], int rt, int n0, in
             if (4 * g + i >= n1) x1[i] = kNegInf;
         }
     }
-    return fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
-                 fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3]))) * f;
+    const float a = fmaxf(fmaxf(x0[0], x0[1]), x0[2]);
+    const float b = fmaxf(fmaxf(a, x0[3]), x1[0]);
+    const float c = fmaxf(fmaxf(b, x1[1]), x1[2]);
+    return fmaxf(c, x1[3]);
 }
 
-// Probabilities of one tile with reference max m (packed for the PV MFMA),
-// and the row sums they add (MFMA against an all-ones operand).
+// dma_lane_max for pages whose K scales (ks0, ks1 > 0) are applied to the
+// scores rather than to K: the max of raw * ks.
+template <int RT, bool PARTIAL>
+__device__ __forceinline__ float dma_lane_max_ks(f4 (&s)[RT][2], int rt, int n0, int n1, int g, float ks0,
+                                                 float ks1) {
+    f4& x0 = s[rt][0];
+    f4& x1 = s[rt][1];
+    if constexpr (PARTIAL) {
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * g + i >= n0) x0[i] = kNegInf;
+            if (4 * g + i >= n1) x1[i] = kNegInf;
+        }
+    }
+    const float r0 = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), x0[2]), x0[3]);
+    const float r1 = fmaxf(fmaxf(fmaxf(x1[0], x1[1]), x1[2]), x1[3]);
+    return fmaxf(r0 * ks0, r1 * ks1);
+}
+
+// The slow path: moves m of every row whose scores passed thr and rescales
+// its accumulators.  Rows that did not move get alpha = 1.
+template <int D, int NRT>
+__device__ __forceinline__ void dma_rescale(const float (&lm)[DmaCfg<D>::RT], RowMax<DmaCfg<D>::RT>& rm,
+                                         f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], float f,
+                                         float finv) {
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        const float mx = rowgroup_max(lm[rt]);
+        if (mx > rm.thr[rt]) {
+            const float mnew = mx * f;
+            const float alpha = rm.m[rt] == kNegInf ? 0.f : fast_exp2(rm.m[rt] - mnew);
+            rm.m[rt] = mnew;
+            rm.thr[rt] = (mnew + kLazyDma) * finv;
+            Lsum[rt] *= alpha;
+            #pragma unroll
+            for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
+        }
+    }
+}
+
+// Probabilities of one tile with reference max m (finite: the item's first
+// pair always sets it), packed for the PV MFMA, and the row sums they add
+// (MFMA against an all-ones operand).
+// f0, f1: the two pages' score factors (f times their K scales when those
+// are applied to the scores).
 template <bool F16>
-__device__ __forceinline__ u32x4 dma_probs(const f4 (&x)[2], float f, float m, f4& L) {
+__device__ __forceinline__ u32x4 dma_probs(const f4 (&x)[2], float f0, float f1, float m, f4& L) {
     const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
     const u32x4 ones = {one2, one2, one2, one2};
-    const float nm = (m == kNegInf) ? 0.f : -m;
+    const float nm = -m;
     float p0[4], p1[4];
     #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        p0[i] = fast_exp2(__builtin_fmaf(x[0][i], f, nm));
-        p1[i] = fast_exp2(__builtin_fmaf(x[1][i], f, nm));
+        p0[i] = fast_exp2(__builtin_fmaf(x[0][i], f0, nm));
+        p1[i] = fast_exp2(__builtin_fmaf(x[1][i], f1, nm));
     }
     const u32x4 pb = {pack2(p0[0], p0[1], F16), pack2(p0[2], p0[3], F16), pack2(p1[0], p1[1], F16),
                       pack2(p1[2], p1[3], F16)};
@@ -1067,16 +1148,15 @@ __device__ __forceinline__ void dma_pair(const AttendArgs& a, const Item& it, co
     }
 }
 
-// K operands of the page pair in slots s0, s0 + PAGE (LDS byte address).
+// K operands of the page pair in the slot at byte offset s (pages at s and
+// s + PAGE from the bases' origin).
 template <int D>
-__device__ __forceinline__ void dma_k_operands(uint32_t s0, const LdsOffsets& lo, u32x4 (&kop)[2][D / 32]) {
+__device__ __forceinline__ void dma_k_operands(uint32_t s, const LdsBases<D>& lb, u32x4 (&kop)[2][D / 32]) {
     using C = DmaCfg<D>;
-    const uint32_t k0 = s0 + lo.k;
     #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
-        const uint32_t ad = k0 ^ uint32_t(kb << 6);
-        kop[0][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(ad));
-        kop[1][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(ad + C::PAGE));
+        kop[0][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(lb.k[kb] + s));
+        kop[1][kb] = *reinterpret_cast<const lds_u32x4*>(uintptr_t(lb.k[kb] + s + C::PAGE));
     }
 }
 
@@ -1097,117 +1177,100 @@ __device__ __forceinline__ void dma_score_mma(const u32x4 (&kop)[2][D / 32],
     }
 }
 
-// Scores of the page pair in slots s0, s0 + PAGE for the wave's NRT tiles.
+// Scores of the page pair in the slot at offset s for the wave's NRT tiles.
 template <int D, bool F16, int NRT>
-__device__ __forceinline__ void dma_scores(uint32_t s0, const LdsOffsets& lo,
+__device__ __forceinline__ void dma_scores(uint32_t s, const LdsBases<D>& lb,
                                            const u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
                                            f4 (&sc)[DmaCfg<D>::RT][2]) {
     u32x4 kop[2][D / 32];
-    dma_k_operands<D>(s0, lo, kop);
+    dma_k_operands<D>(s, lb, kop);
     dma_score_mma<D, F16, NRT>(kop, qB, sc);
 }
 
-// The transposed V operands of the page pair in slots s0, s0 + PAGE, all
+// The transposed V operands of the page pair in the slot at offset s, all
 // d-blocks at once (read before the scores so they land behind the MFMAs).
 template <int D>
-__device__ __forceinline__ void dma_v_operands(uint32_t s0, const LdsOffsets& lo, u32x4 (&vop)[D / 16]) {
+__device__ __forceinline__ void dma_v_operands(uint32_t s, const LdsBases<D>& lb, u32x4 (&vop)[D / 16]) {
     using C = DmaCfg<D>;
-    const uint32_t v00 = s0 + lo.v;
     #pragma unroll
     for (int e = 0; e < D / 16; ++e) {
-        const uint32_t ad = v00 ^ uint32_t(e << 5);
+        const uint32_t ad = lb.v[e] + s;
         const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(ad));
         const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(ad + C::PAGE));
         vop[e] = __builtin_shufflevector(__builtin_bit_cast(u32x2, v0), __builtin_bit_cast(u32x2, v1), 0, 1, 2, 3);
     }
 }
 
-// O^T += V^T P^T with operands already in registers.
-template <int D, bool F16, int NRT, bool TAIL>
-__device__ __forceinline__ void dma_pv_regs(u32x4 (&vop)[D / 16], bool partial, int n0, int n1, int g,
-                                            const u32x4 (&pB)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16]) {
+// One step of the pair loop after its barrier: the lazy-max check of pair
+// p (scores already in sc) and its rare rescale, then the LDS reads (V of
+// pair p from the slot at offset vs and, when NEXT, K of pair p + 1 from the
+// slot at ks), the score MFMAs of pair p + 1 interleaved with the softmax of
+// pair p, and the PV MFMAs.  PART masks tokens past n0 / n1 (the item's
+// last pair only); the last pair has no next pair (NEXT false).  KS: the
+// pages' K scales ks0, ks1 multiply the scores (K was staged unscaled).
+template <int D, bool F16, int NRT, bool PART, bool NEXT, bool KS = false>
+__device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, int n0, int n1, const LdsBases<D>& lb,
+                                         const u32x4 (&qB)[DmaCfg<D>::RT][D / 32], f4 (&sc)[DmaCfg<D>::RT][2],
+                                         u32x4 (&vop)[D / 16], RowMax<DmaCfg<D>::RT>& rm,
+                                         f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], int g,
+                                         float f, float finv, float ks0 = 1.f, float ks1 = 1.f) {
+    constexpr int RT = DmaCfg<D>::RT, KB = D / 32;
+    bool need = false;
+    float lm[RT];
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        if constexpr (KS) lm[rt] = dma_lane_max_ks<RT, PART>(sc, rt, n0, n1, g, ks0, ks1);
+        else lm[rt] = dma_lane_max<RT, PART>(sc, rt, n0, n1, g);
+        need |= lm[rt] > rm.thr[rt];
+    }
+    if (__ballot(need)) dma_rescale<D, NRT>(lm, rm, Lsum, O, f, finv);
+    // Branch-free from here, so the scheduler sees one region: LDS reads
+    // first, then the score MFMAs of pair p + 1 interleaved with the
+    // softmax of pair p (a wave overlaps some of its VALU work with MFMAs
+    // in flight), then the PV MFMAs.
+    __builtin_amdgcn_sched_barrier(0);
+    dma_v_operands<D>(vs, lb, vop);
+    if constexpr (PART) {
+        #pragma unroll
+        for (int e = 0; e < D / 16; ++e) {
+            mask_v_tr(vop[e], 0, g, n0);
+            mask_v_tr(vop[e], 2, g, n1);
+        }
+    }
+    u32x4 kop[2][KB];
+    if constexpr (NEXT) dma_k_operands<D>(ks, lb, kop);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 pB[RT];
+    const float f0 = KS ? f * ks0 : f, f1 = KS ? f * ks1 : f;
+    #pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f0, f1, rm.m[rt], Lsum[rt]);
+    if constexpr (NEXT) {
+        dma_score_mma<D, F16, NRT>(kop, qB, sc);
+        #pragma unroll
+        for (int k = 0; k < NRT * 2 * KB; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     #pragma unroll
     for (int e = 0; e < D / 16; ++e) {
-        if constexpr (TAIL) {
-            if (partial) {
-                mask_v_tr(vop[e], 0, g, n0);
-                mask_v_tr(vop[e], 2, g, n1);
-            }
-        }
         #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
     }
 }
 
-// One iteration of the pair loop after its barrier: the lazy-max check of
-// pair pi (scores already in sc) and its rare rescale, then the LDS reads
-// (V of pair pi from slot vslot, K of pair pi + 1 from slot kslot), the score
-// MFMAs of pair pi + 1 interleaved with the softmax of pair pi, and the PV
-// MFMAs.  On the last pair kslot is stale and the scores it gives are unused.
-template <int D, bool F16, int NRT, bool TAIL>
-__device__ __forceinline__ void dma_step(uint32_t vslot, uint32_t kslot, int n0, int n1, const LdsOffsets& lo,
-                                         const u32x4 (&qB)[DmaCfg<D>::RT][D / 32], f4 (&sc)[DmaCfg<D>::RT][2],
-                                         u32x4 (&vop)[D / 16], float (&m)[DmaCfg<D>::RT],
-                                         f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], int g,
-                                         float f) {
-    constexpr int RT = DmaCfg<D>::RT, KB = D / 32;
-    const bool partial = (n0 != kPageSize) || (n1 != kPageSize);
-    // A row's reference max moves only when a score passes it by
-    // kLazyDma (always on the item's first pair, where m is -inf).
-    bool need = false;
-    float lm[RT];
-    #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-        lm[rt] = partial ? dma_lane_max<RT, true>(sc, rt, n0, n1, g, f)
-                         : dma_lane_max<RT, false>(sc, rt, n0, n1, g, f);
-        need |= lm[rt] > m[rt] + kLazyDma;
-    }
-    if (__ballot(need)) {
-        #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const float mx = rowgroup_max(lm[rt]);
-            const float mnew = mx > m[rt] + kLazyDma ? mx : m[rt];
-            const float alpha = (m[rt] == kNegInf) ? 0.f : fast_exp2(m[rt] - mnew);
-            m[rt] = mnew;
-            Lsum[rt] *= alpha;
-            #pragma unroll
-            for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
-        }
-    }
-    if constexpr (TAIL) {
-        if (partial) {
-            dma_v_operands<D>(vslot, lo, vop);
-            #pragma unroll
-            for (int e = 0; e < D / 16; ++e) {
-                mask_v_tr(vop[e], 0, g, n0);
-                mask_v_tr(vop[e], 2, g, n1);
-            }
-        }
-    }
-    // Branch-free from here, so the scheduler sees one region: LDS
-    // reads first, then the score MFMAs of pair pi + 1 interleaved
-    // with the softmax of pair pi, then the PV MFMAs.  On the last
-    // pair the K reads and score MFMAs run on a stale slot and
-    // their result is never used.
-    __builtin_amdgcn_sched_barrier(0);
-    if (!(TAIL && partial)) dma_v_operands<D>(vslot, lo, vop);
-    u32x4 kop[2][KB];
-    dma_k_operands<D>(kslot, lo, kop);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 pB[RT];
-    #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f, m[rt], Lsum[rt]);
-    dma_score_mma<D, F16, NRT>(kop, qB, sc);
-    #pragma unroll
-    for (int k = 0; k < NRT * 2 * KB; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    #pragma unroll
-    for (int e = 0; e < D / 16; ++e) {
-        #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
+// Compile-time loop index.
+template <int J>
+struct Idx {
+    static constexpr int value = J;
+};
+
+template <int J, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (J < N) {
+        f(Idx<J>{});
+        static_for<J + 1, N>(f);
     }
 }
 
@@ -1240,7 +1303,7 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
                                                uint8_t* ring, int tid, int wave, int g, int c,
                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
                                                u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
-                                               float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
+                                               RowMax<DmaCfg<D>::RT>& rm, f4 (&Lsum)[DmaCfg<D>::RT],
                                                f4 (&O)[DmaCfg<D>::RT][D / 16]) {
     using C = DmaCfg<D>;
     constexpr uint32_t P = C::NP, QS = C::QSLOTS;
@@ -1257,8 +1320,11 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
         const int j = pos ^ chunk_swz<D>(row);
         src.loff[u] = uint32_t((plane * a.hkv + it.kv_head) * C::PLANE + row * C::RB + j * 16);
     }
-    const LdsOffsets lo = lds_offsets<D>(g, c);
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
+    const LdsBases<D> lb = lds_bases<D>(ring_lds, g, c);
+    const float f = a.scale_log2;   // > 0 (a negative scale is in q_sign)
+    const float finv = 1.f / f;
+    const uint32_t qsign = a.q_sign;
     // Every load the compiler issued (row targets, page ids) has landed
     // before the ring loads start, so no compiler-inserted wait can drain
     // the ring.
@@ -1283,7 +1349,7 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
             const bool valid = uint32_t(rt * kWaves + wave) * kTileRows + c < it.nrows;
             #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024) ^ qsign;
                 qB[rt][kb] = valid ? v : u32x4{0u, 0u, 0u, 0u};
             }
         }
@@ -1291,54 +1357,58 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
     block_barrier();   // every wave holds its query rows: their slots take pages
     #pragma unroll 1
     for (uint32_t q = pro; q < min(P - 1, npairs); ++q) dma_pair<D>(a, it, ids, src, ring_lds, q, q, wave);
-    // Software pipeline: iteration pi computes the scores of pair pi + 1
-    // while it finishes pair pi.  It reads K of pair pi + 1 and V of pair
-    // pi; after its barrier the slot of pair pi - 1 is free and takes pair
-    // pi + P - 1.  Issued before iteration pi: pairs < min(pi + P - 1, npairs).
-    // Order inside an iteration (pinned with scheduling barriers, since a
-    // wave issues in order): the row-max check of pair pi (its scores are
+    // Software pipeline: step pi computes the scores of pair pi + 1 while
+    // it finishes pair pi.  It reads K of pair pi + 1 and V of pair pi;
+    // after its barrier the slot of pair pi - 1 is free and takes pair
+    // pi + P - 1.  Pair p sits in slot p % P, so the steps are unrolled
+    // over the P slots and every LDS read takes its slot as an immediate
+    // offset.  Issued before step pi: pairs < min(pi + P - 1, npairs).
+    // Order inside a step (pinned with scheduling barriers, since a wave
+    // issues in order): the row-max check of pair pi (its scores are
     // already in registers) and the rare rescale; then all LDS reads; then
-    // the probabilities of pair pi (VALU), which cover the LDS latency; then
-    // the score MFMAs of pair pi + 1 and the PV MFMAs of pair pi.
+    // the probabilities of pair pi (VALU) interleaved with the score MFMAs
+    // of pair pi + 1; then the PV MFMAs of pair pi.  The last pair runs
+    // apart: it may hold partial pages and has no next pair to score.
     constexpr int RT = C::RT;
-    const float f = a.scale_log2;
+    constexpr uint32_t SLOT = 2 * C::PAGE;
     f4 sc[RT][2];
     u32x4 vop[D / 16];
     wait_vmcnt((min(P - 1, npairs) - 1) * C::PER_PAIR);   // pair 0 has landed
     block_barrier();
-    if constexpr (NRT > 0) dma_scores<D, F16, NRT>(ring_lds, lo, qB, sc);
-    uint32_t ps = 0, psn = 1;   // slots of pairs pi, pi + 1
+    if constexpr (NRT > 0) dma_scores<D, F16, NRT>(0, lb, qB, sc);
     // Page ids of the pair the next refill loads (pair pi + P - 1), read from
-    // LDS an iteration ahead so the refill does not wait on them.
-    uint32_t nid0 = 0, nid1 = 0;
-    {
-        const uint32_t i0 = min(2 * (P - 1), np - 1), i1 = min(2 * (P - 1) + 1, np - 1);
-        nid0 = ids[i0];
-        nid1 = ids[i1];
-    }
+    // LDS a step ahead so the refill does not wait on them.
+    uint32_t nid0 = ids[min(2 * (P - 1), np - 1)];
+    uint32_t nid1 = ids[min(2 * (P - 1) + 1, np - 1)];
+    const uint32_t nmain = npairs - 1;
     #pragma unroll 1
-    for (uint32_t pi = 0; pi < npairs; ++pi) {
-        if (pi + P - 1 <= npairs) wait_vmcnt_const<(P - 3) * C::PER_PAIR>();   // pair pi + 1 has landed
-        else if (pi + 1 < npairs) wait_vmcnt((npairs - pi - 2) * C::PER_PAIR);
-        block_barrier();
-        if (pi + P - 1 < npairs)
-            dma_pair_pages<D>(a, __builtin_amdgcn_readfirstlane(nid0), __builtin_amdgcn_readfirstlane(nid1), src,
-                              ring_lds, ps == 0 ? P - 1 : ps - 1, wave);
-        {
-            const uint32_t i0 = min(2 * (pi + P), np - 1), i1 = min(2 * (pi + P) + 1, np - 1);
-            nid0 = ids[i0];
-            nid1 = ids[i1];
-        }
-        if constexpr (NRT > 0) {
-            const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
-            const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
-            dma_step<D, F16, NRT, TAIL>(ring_lds + ps * 2 * C::PAGE, ring_lds + psn * 2 * C::PAGE, n0, n1, lo, qB,
-                                        sc, vop, m, Lsum, O, g, f);
-        }
-        ps = psn;
-        psn = psn + 1 == P ? 0 : psn + 1;
+    for (uint32_t p0 = 0; p0 < nmain; p0 += P) {
+        static_for<0, int(P)>([&](auto J) {
+            constexpr uint32_t j = decltype(J)::value;
+            const uint32_t pi = p0 + j;
+            if (pi >= nmain) return;
+            if (pi + P - 1 <= npairs) wait_vmcnt_const<(P - 3) * C::PER_PAIR>();   // pair pi + 1 has landed
+            else wait_vmcnt((npairs - pi - 2) * C::PER_PAIR);
+            block_barrier();
+            if (pi + P - 1 < npairs)
+                dma_pair_pages<D>(a, __builtin_amdgcn_readfirstlane(nid0), __builtin_amdgcn_readfirstlane(nid1),
+                                  src, ring_lds, (j + P - 1) % P, wave);
+            nid0 = ids[min(2 * (pi + P), np - 1)];
+            nid1 = ids[min(2 * (pi + P) + 1, np - 1)];
+            if constexpr (NRT > 0)
+                dma_step<D, F16, NRT, false, true>(j * SLOT, ((j + 1) % P) * SLOT, kPageSize, kPageSize, lb, qB, sc,
+                                                   vop, rm, Lsum, O, g, f, finv);
+        });
     }
-    // The last pair's wait was vmcnt(0): no ring load is outstanding.
+    // The last pair: its loads were waited for (vmcnt(0)) and made visible
+    // by the previous step's barrier (or the prologue's); it refills nothing
+    // and reads no K, so it needs no barrier of its own.
+    if constexpr (NRT > 0) {
+        const uint32_t pl = nmain;
+        const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
+        const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
+        dma_step<D, F16, NRT, true, false>((pl % P) * SLOT, 0, n0, n1, lb, qB, sc, vop, rm, Lsum, O, g, f, finv);
+    }
 }
 
 // Query rows of a wave's tiles in a DMA group item: tile rt of wave w covers
@@ -1380,21 +1450,22 @@ __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& i
     using C = DmaCfg<D>;
     constexpr int RT = C::RT, EPL = D / 16, KB = D / 32;
     u32x4 qB[RT][KB];
-    float m[RT];
+    RowMax<RT> rm;
     f4 L[RT];
     f4 O[RT][EPL];
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = kNegInf;
+        rm.m[rt] = kNegInf;
+        rm.thr[rt] = kNegInf;
         L[rt] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
     if (it.flags & kItemTail)
-        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
+        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
     else
-        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
-    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, m, L, O, g, c);
+        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
+    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
 }
 
 // Item fields as wave-uniform values (they are: the item is the workgroup's),
@@ -1440,9 +1511,10 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
 // into a bf16 pair slot laid out as the 16-bit path's (swizzled rows), and
 // the 16-bit pair loop's compute (dma_step) runs on those slots.  MXFP8
 // elements take their E8M0 group scale in the exact power-of-two conversion;
-// E4M3 with a block scale is converted exactly to f32, multiplied by the
-// scale and rounded to bf16: K and V dequantised to the query dtype, as
-// ReferenceBackend computes them.  Per iteration pi: wait for raw pair
+// with an E4M3 block scale, K codes are converted exactly (the scale then
+// multiplies the scores, so a large attention scale cannot amplify a
+// rounding of code * scale) and V is converted exactly to f32, multiplied
+// by its scale and rounded once to bf16.  Per iteration pi: wait for raw pair
 // pi + 1, barrier, refill the raw slot of pair pi - 1 (converted two
 // iterations ago), convert raw pair pi + 1 into bf16 slot (pi + 1) & 1,
 // barrier, compute.  Head_dim 128 and 256 (64 keeps the register path).
@@ -1573,7 +1645,15 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
             const float sc = e8m0_to_float(scl[(page * 2 + plane) * C8::SREC + row * (D / 32) + col0 / 32]);
             #pragma unroll
             for (int w = 0; w < 8; ++w) e4m3x4_to_bf16(wd[w], sc, out[2 * w], out[2 * w + 1]);
+        } else if (plane == 0) {
+            // K: the codes alone (exact in bf16); the block scale multiplies
+            // the scores, so the attention scale does not amplify a rounding
+            // of code * scale.  (plane is wave-uniform: a wave converts 2048
+            // consecutive bytes, whole planes at head_dim 128 and 256.)
+            #pragma unroll
+            for (int w = 0; w < 8; ++w) e4m3x4_to_bf16(wd[w], 1.f, out[2 * w], out[2 * w + 1]);
         } else {
+            // V: code * scale in f32, rounded once to bf16 (RNE).
             const float sc = *reinterpret_cast<const float*>(scl + 4 * (page * 2 + plane));
             #pragma unroll
             for (int w = 0; w < 8; ++w) {
@@ -1597,7 +1677,7 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
                                                 uint8_t* ring, int tid, int wave, int g, int c,
                                                 const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
                                                 u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
-                                                float (&m)[DmaCfg<D>::RT], f4 (&Lsum)[DmaCfg<D>::RT],
+                                                RowMax<DmaCfg<D>::RT>& rm, f4 (&Lsum)[DmaCfg<D>::RT],
                                                 f4 (&O)[DmaCfg<D>::RT][D / 16]) {
     using C = DmaCfg<D>;
     using C8 = Dma8Cfg<D>;
@@ -1607,9 +1687,21 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
     const uint32_t npairs = (np + 1) >> 1;
     const int lane = tid & 63;
     const Dma8Src<D> src = dma8_src<D, KVF>(a, it, wave, lane);
-    const LdsOffsets lo = lds_offsets<D>(g, c);
     const uint32_t raw_lds = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(ring)));
     const uint32_t bf_lds = raw_lds + C8::RAW_BYTES;
+    const LdsBases<D> lb = lds_bases<D>(bf_lds, g, c);
+    const float f = a.scale_log2;   // > 0 (a negative scale is in q_sign)
+    const float finv = 1.f / f;
+    const uint32_t qsign = a.q_sign;
+    // FP8 block scale: K is staged unscaled and the pages' K scales (in the
+    // raw slot of the pair being finished, records [page][K|V]) multiply
+    // the scores.
+    constexpr bool KS = KVF == KVF_FP8;
+    auto k_scales = [&](uint32_t rs, float& k0, float& k1) {
+        const float* sk = reinterpret_cast<const float*>(ring + rs * (C8::RAW_PAIR + C8::SCALES) + C8::RAW_PAIR);
+        k0 = sk[0];
+        k1 = sk[2];
+    };
     auto page_id = [&](uint32_t i) { return __builtin_amdgcn_readfirstlane(ids[i < np ? i : np - 1]); };
     // Every compiler-issued load (row targets, page ids) has landed before
     // the ring loads start, so no compiler-inserted wait drains the ring.
@@ -1633,7 +1725,7 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
             const bool valid = uint32_t(rt * kWaves + wave) * kTileRows + c < it.nrows;
             #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(qw + (rt * KB + kb) * 1024) ^ qsign;
                 qB[rt][kb] = valid ? v : u32x4{0u, 0u, 0u, 0u};
             }
         }
@@ -1642,31 +1734,51 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
     block_barrier();                             // query rows read; raw pair 0 visible
     dma8_convert<D, KVF>(ring, 0, 0, tid);
     block_barrier();
-    const float f = a.scale_log2;
     f4 sc[RT][2];
     u32x4 vop[D / 16];
-    if constexpr (NRT > 0) dma_scores<D, false, NRT>(bf_lds, lo, qB, sc);
+    if constexpr (NRT > 0) dma_scores<D, false, NRT>(0, lb, qB, sc);
     uint32_t ps = 0, psn = 1;   // raw slots of pairs pi, pi + 1
     uint32_t nid0 = page_id(2 * (P - 1)), nid1 = page_id(2 * (P - 1) + 1);
+    // Step pi: raw pair pi + 1 is converted into bf16 slot (pi + 1) & 1 while
+    // pair pi is finished from slot pi & 1; steps are unrolled by two so the
+    // bf16 slots are immediate offsets.  The last pair runs apart (partial
+    // pages, nothing to score next, nothing to convert).
+    const uint32_t nmain = npairs - 1;
     #pragma unroll 1
-    for (uint32_t pi = 0; pi < npairs; ++pi) {
-        if (pi + 1 < npairs) wait_vmcnt_any((min(pi + P - 1, npairs) - pi - 2) * C8::PER_PAIR);   // raw pair pi + 1
-        block_barrier();
-        if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
-        nid0 = page_id(2 * (pi + P));
-        nid1 = page_id(2 * (pi + P) + 1);
-        if (pi + 1 < npairs) dma8_convert<D, KVF>(ring, psn, (pi + 1) & 1, tid);
-        block_barrier();
-        if constexpr (NRT > 0) {
-            const int n0 = TAIL && 2 * pi + 1 == np ? last_len : kPageSize;
-            const int n1 = 2 * pi + 1 >= np ? 0 : (TAIL && 2 * pi + 2 == np ? last_len : kPageSize);
-            dma_step<D, false, NRT, TAIL>(bf_lds + (pi & 1) * C8::BF_PAIR, bf_lds + ((pi + 1) & 1) * C8::BF_PAIR,
-                                          n0, n1, lo, qB, sc, vop, m, Lsum, O, g, f);
-        }
-        ps = psn;
-        psn = psn + 1 == P ? 0 : psn + 1;
+    for (uint32_t p0 = 0; p0 < nmain; p0 += 2) {
+        static_for<0, 2>([&](auto J) {
+            constexpr uint32_t j = decltype(J)::value;
+            const uint32_t pi = p0 + j;
+            if (pi >= nmain) return;
+            wait_vmcnt_any((min(pi + P - 1, npairs) - pi - 2) * C8::PER_PAIR);   // raw pair pi + 1
+            block_barrier();
+            if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
+            nid0 = page_id(2 * (pi + P));
+            nid1 = page_id(2 * (pi + P) + 1);
+            dma8_convert<D, KVF>(ring, psn, (j + 1) & 1, tid);
+            block_barrier();
+            if constexpr (NRT > 0) {
+                float ks0 = 1.f, ks1 = 1.f;
+                if constexpr (KS) k_scales(ps, ks0, ks1);
+                dma_step<D, false, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR, kPageSize,
+                                                         kPageSize, lb, qB, sc, vop, rm, Lsum, O, g, f, finv, ks0,
+                                                         ks1);
+            }
+            ps = psn;
+            psn = psn + 1 == P ? 0 : psn + 1;
+        });
     }
-    // The last wait was vmcnt(0): no ring load is outstanding.
+    // The last pair was converted and made visible by the previous step (or
+    // the prologue); every raw load has landed (the last wait was vmcnt(0)).
+    if constexpr (NRT > 0) {
+        const uint32_t pl = nmain;
+        const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
+        const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
+        float ks0 = 1.f, ks1 = 1.f;
+        if constexpr (KS) k_scales(ps, ks0, ks1);
+        dma_step<D, false, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, n0, n1, lb, qB, sc, vop, rm, Lsum, O,
+                                                g, f, finv, ks0, ks1);
+    }
 }
 
 template <int D, uint32_t KVF, int NRT>
@@ -1676,21 +1788,22 @@ __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& 
     using C = DmaCfg<D>;
     constexpr int RT = C::RT, EPL = D / 16, KB = D / 32;
     u32x4 qB[RT][KB];
-    float m[RT];
+    RowMax<RT> rm;
     f4 L[RT];
     f4 O[RT][EPL];
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = kNegInf;
+        rm.m[rt] = kNegInf;
+        rm.thr[rt] = kNegInf;
         L[rt] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
     if (it.flags & kItemTail)
-        dma8_group_loop<D, KVF, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
+        dma8_group_loop<D, KVF, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
     else
-        dma8_group_loop<D, KVF, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, m, L, O);
-    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, m, L, O, g, c);
+        dma8_group_loop<D, KVF, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
+    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
 }
 
 template <int D, uint32_t KVF>
@@ -1755,6 +1868,8 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
         dst[0] = slot * a.hq + qh;
         const float* qp = reinterpret_cast<const float*>(a.q) + (uint64_t(seq) * a.hq + qh) * D + g * KQ;
         load_dwords<KQ>(reinterpret_cast<uint32_t*>(qv), qp);
+        #pragma unroll
+        for (int k = 0; k < KQ; ++k) qv[k] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, qv[k]) ^ a.q_sign);
     } else {
         #pragma unroll
         for (int k = 0; k < KQ; ++k) qv[k] = 0.f;

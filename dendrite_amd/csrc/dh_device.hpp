@@ -90,7 +90,11 @@ struct AttendArgs {
                                  // else f16 scaled per row by 2^-k
     PartialLse* ws_lse;          // [slots][Hq]
     uint32_t hq, hkv, r, gqa_tiled;
-    float scale_log2;            // softmax scale * log2(e)
+    float scale_log2;            // |softmax scale| * log2(e), at least 2^-60 (> 0)
+    uint32_t q_sign;             // XOR mask on the query elements' sign bits: a
+                                 // negative scale is folded into the query, so the
+                                 // kernels see scale_log2 > 0 and may order scaled
+                                 // scores by raw ones
     uint32_t n_group_items, n_wave_items;
 };
 

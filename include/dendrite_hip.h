@@ -105,7 +105,8 @@ typedef struct dh_attn_config {
     uint32_t num_heads;       /* query heads                                   */
     uint32_t num_kv_heads;    /* KV heads; num_heads % num_kv_heads == 0       */
     uint32_t head_dim;        /* 64, 128 or 256 (flashinfer/mod.rs:20)         */
-    float scale;              /* softmax scale, 1/sqrt(head_dim) by default    */
+    float scale;              /* softmax scale, 1/sqrt(head_dim) by default;
+                                 any finite value (0 gives uniform weights)   */
     uint32_t sliding_window;  /* 0 = None.  Accepted and ignored, as by every
                                  Dendrite backend (backend.rs:206-265 never
                                  reads it): attention spans all tokens.       */
@@ -161,7 +162,8 @@ void* dh_pool_scales(dh_pool* pool);
 
 /* Write tokens [tok_offset, tok_offset + n_tok) of one page from host memory.
  * k, v: [num_kv_heads][n_tok][head_dim] elements of the pool's format.
- * k_scale/v_scale: FP8_E4M3: float[num_kv_heads] (replaces the page's scale);
+ * k_scale/v_scale: FP8_E4M3: float[num_kv_heads] (replaces the page's scale;
+ * every FP8 block scale must be finite and > 0, else DH_EINVAL);
  * MXFP8: uint8[num_kv_heads][n_tok][head_dim/32]; ignored otherwise.
  * This is the device half of ReferenceBackend::append_kv/store_kv
  * (attention/backend.rs:285-301, 140-143) and Page::append (paged.rs:156-183).

@@ -18,7 +18,7 @@ def q_tensor(q_raw: np.ndarray, q_dtype: int, device: str = "cuda:0"):
 class GpuRun:
     """Uploads a workload's pages and runs one decode step."""
 
-    def __init__(self, w, backend: Backend, cascade: bool = True, ids=None, **plan_kw):
+    def __init__(self, w, backend: Backend, cascade: bool = True, ids=None, scale=None, **plan_kw):
         import torch
         self.w = w
         self.backend = backend
@@ -27,6 +27,8 @@ class GpuRun:
         self.data, self.scales = w.make_pages(self.ids)
         self.pool.write_pages(self.ids, self.data, self.scales)
         self.cfg = w.attention_config()
+        if scale is not None:
+            self.cfg.scale = float(scale)
         self.plan = DecodePlan(backend, self.cfg, self.pool, w.indptr, w.indices, cascade=cascade,
                                **plan_kw)
         self.q_raw = w.make_q()

@@ -209,3 +209,24 @@ def test_decode_rejects_bad_workspace(backend):
     with pytest.raises(DhError) as e:
         decode_batch(plan, q, out, small)
     assert e.value.status == _lib.DH_EINVAL
+
+
+@pytest.mark.parametrize("bad", [0.0, -1.0, float("nan"), float("inf")])
+def test_fp8_block_scales_must_be_positive(backend, bad):
+    """FP8 E4M3 block scales are finite and > 0 (the quantiser's amax / 448,
+    1 for an all-zero block); others are rejected on write, before any copy."""
+    hkv, d = 2, 128
+    pool = Pool(backend, 8, hkv, d, _lib.KV_FP8_E4M3)
+    data = np.zeros((1, pool.page_bytes), dtype=np.uint8)
+    scales = np.ones((1, 2 * hkv), dtype=np.float32)
+    pool.write_pages([3], data, scales.view(np.uint8))
+    scales[0, 1] = bad
+    with pytest.raises(DhError) as e:
+        pool.write_pages([3], data, scales.view(np.uint8))
+    assert e.value.status == _lib.DH_EINVAL
+    k = np.zeros((hkv, 16, d), dtype=np.uint8)
+    with pytest.raises(DhError):
+        pool.write_tokens(3, 0, k, k, k_scale=np.array([1.0, bad], np.float32),
+                          v_scale=np.ones(hkv, np.float32))
+    _, s = pool.read_page(3)
+    assert np.array_equal(s.view(np.float32), np.ones(2 * hkv, np.float32))

@@ -89,3 +89,15 @@ def test_random_trees(backend, shape, fmt):
     for seed in (11, 12):
         w = workloads.random_tree(seed, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
         _check(w, backend, cascade=(seed % 2 == 1))
+
+
+@pytest.mark.parametrize("scale", [-0.25, 0.0, 1.5], ids=["negative", "zero", "large"])
+@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("fmt", [FORMATS[0], FORMATS[1], FORMATS[3], FORMATS[4]], ids=["bf16", "f16", "fp8", "mxfp8"])
+def test_scales(backend, shape, fmt, scale):
+    """Scales other than 1/sqrt(D): a negative scale (folded into the query's
+    sign on the shared-prefix path), zero (uniform weights) and a large one
+    (scores spread over tens of log2 units, so the running max moves often)."""
+    hq, hkv, d = shape
+    w = workloads.random_tree(21, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
+    _check(w, backend, scale=scale)
