@@ -101,3 +101,17 @@ def test_scales(backend, shape, fmt, scale):
     hq, hkv, d = shape
     w = workloads.random_tree(21, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
     _check(w, backend, scale=scale)
+
+
+def test_empty_sequences(backend):
+    """Sequences without pages get zeros (backend.rs:218-222), also when no
+    sequence of the batch has a page (no attention item at all)."""
+    for tables in ([[], [3, 4, 5], []], [[], []]):
+        w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 64)
+        run = GpuRun(w, backend)
+        run.out.fill_(7.0)
+        got = run.run()
+        for b, t in enumerate(tables):
+            if not t:
+                assert not np.any(got[b]), f"sequence {b} without pages is not zero"
+        assert excess_err(got, run.reference(), w.q_dtype) <= TOL[w.q_dtype]
