@@ -101,6 +101,42 @@ def measured_traffic(workload: str):
     return t.get("hbm_bytes_per_launch")
 
 
+def bench_write(args):
+    """Quantise-on-write throughput: N bf16 pages [2][Hkv][16][D] resident in
+    HBM into a pool of the workload's shape and format, through
+    dh_pool_write_pages_device.  Bytes per page: the bf16 source read, the
+    page and its scale record written."""
+    import torch
+    from dendrite_amd import workloads
+    from dendrite_amd.backend import Backend, Pool
+    w = workloads.ALL[args.workload]()
+    n = args.write_pages
+    be = Backend(0)
+    pool = Pool(be, n, w.hkv, w.d, w.kv_format)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    src = torch.randn((n, 2, w.hkv, 16, w.d), generator=g, device="cuda").to(torch.bfloat16)
+    ids = torch.randperm(n, device="cuda").to(torch.int32)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        pool.write_pages_device(ids, src, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        pool.write_pages_device(ids, src, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    per_page = src[0].numel() * 2 + pool.page_bytes + pool.scale_bytes
+    gbs = n * per_page / (us * 1e-6) / 1e9
+    print(json.dumps({"metric": "quantise-on-write page throughput", "value": round(gbs, 2), "unit": "GB/s",
+                      "us_per_call": round(us, 3), "pages": n, "bytes_per_page": per_page,
+                      "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
+                      "config": {"workload": w.name, "num_kv_heads": w.hkv, "head_dim": w.d,
+                                 "kv_format": w.kv_format, "source": "bf16"},
+                      "steps": args.steps, "warmup": args.warmup}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +148,9 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--write-pages", type=int, default=0, metavar="N",
+                    help="only measure quantise-on-write (dh_pool_write_pages_device) of N bf16 pages "
+                         "into a pool of the workload's shape and KV format")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -135,6 +174,10 @@ def main():
         return
 
     from dendrite_amd.backend import Backend, DecodePlan, Pool, decode_batch, raw_to_tensor
+
+    if args.write_pages:
+        bench_write(args)
+        return
 
     ws_list = build_workloads(args.workload, args.rotations)
     w0 = ws_list[0]

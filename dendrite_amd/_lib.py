@@ -103,6 +103,7 @@ SIGNATURES = {
     "dh_pool_scales": (_P, [_P]),
     "dh_pool_write_tokens": (_I, [_P, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "dh_pool_write_pages": (_I, [_P, _PU32, _U32, _P, _P, _P]),
+    "dh_pool_write_pages_device": (_I, [_P, _P, _U32, _P, _U32, _P]),
     "dh_pool_copy_page": (_I, [_P, _U32, _U32, _P]),
     "dh_pool_read_page": (_I, [_P, _U32, _P, _P]),
     "dh_plan_create": (_I, [_P, C.POINTER(dh_attn_config), _P, _PU32, _PU32, _U32, _U32,

@@ -167,6 +167,28 @@ class Pool:
                                         data.ctypes.data_as(C.c_void_p), sp,
                                         _stream_ptr(stream) if stream is not None else None))
 
+    def write_pages_device(self, page_ids, src, stream=None) -> None:
+        """Quantise-on-write from device tensors: page_ids (uint32 / int32,
+        [n]) receive src ([n, 2, num_kv_heads, 16, head_dim] float32 /
+        bfloat16 / float16, K then V, zero past a partial page's tokens) in
+        the pool's format (dh_pool_write_pages_device).  Ids outside the pool
+        are skipped."""
+        torch = _torch()
+        dtype = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
+                 torch.float16: _lib.DTYPE_F16}.get(src.dtype)
+        if dtype is None:
+            raise DhError(_lib.DH_EINVAL, f"source dtype {src.dtype} (float32, bfloat16 or float16)")
+        want = (2, self.num_kv_heads, _lib.PAGE_SIZE, self.head_dim)
+        if src.dim() != 5 or tuple(src.shape[1:]) != want or src.shape[0] != page_ids.numel():
+            raise DhError(_lib.DH_EINVAL, f"src shape {tuple(src.shape)} is not [n, *{want}]")
+        if not (src.is_cuda and page_ids.is_cuda and src.is_contiguous() and page_ids.is_contiguous()):
+            raise DhError(_lib.DH_EINVAL, "page_ids and src must be contiguous device tensors")
+        if page_ids.dtype not in (torch.int32, torch.uint32):
+            raise DhError(_lib.DH_EINVAL, "page_ids must be int32 or uint32")
+        check(lib().dh_pool_write_pages_device(self._h, C.c_void_p(page_ids.data_ptr()), page_ids.numel(),
+                                               C.c_void_p(src.data_ptr()), dtype,
+                                               _stream_ptr(stream) if stream is not None else None))
+
     def write_tokens(self, page_id: int, tok_offset: int, k: np.ndarray, v: np.ndarray,
                      k_scale=None, v_scale=None, stream=None) -> None:
         """k, v: [num_kv_heads][n_tok][head_dim] in the pool's element format."""
@@ -312,10 +334,41 @@ class HipBackend:
         self.pool = Pool(self.backend, num_pages, num_kv_heads, head_dim, kv_format)
         self.cascade = cascade
         self.page_len: dict[int, int] = {}
+        # FP8 pools: the f32 tokens of each page still being filled, so an
+        # append re-quantises the page from all its tokens (a block scale
+        # covers the whole page); dropped once the page holds 16 tokens.
+        self._shadow: dict = {}
 
     @classmethod
     def new(cls, **kw) -> "HipBackend":
         return cls(**kw)
+
+    def _append_quantised(self, page: int, off: int, key, value) -> int:
+        """Writes tokens off.. of an FP8 / MXFP8 page: the page's f32 tokens
+        so far plus these, quantised on the device (Pool.write_pages_device)."""
+        torch = _torch()
+        dev = f"cuda:{self.backend.device}"
+        k, v = key.detach(), value.detach()
+        if k.dim() == 4:
+            k, v = k[0], v[0]
+        hkv, d = self.pool.num_kv_heads, self.pool.head_dim
+        n = k.shape[1]
+        if tuple(k.shape) != (hkv, n, d) or tuple(v.shape) != (hkv, n, d) or off + n > _lib.PAGE_SIZE:
+            raise DhError(_lib.DH_EINVAL, f"key shape {tuple(key.shape)} at offset {off} does not fit the page")
+        sh = self._shadow.get(page)
+        if off == 0 or sh is None:
+            if off != 0 and self.page_len.get(page, 0) > 0:
+                raise DhError(_lib.DH_EUNSUPPORTED, f"FP8 page {page} is complete; rewrite it from offset 0")
+            sh = torch.zeros((1, 2, hkv, _lib.PAGE_SIZE, d), dtype=torch.float32, device=dev)
+        sh[0, 0, :, off:off + n] = k.to(dev, torch.float32)
+        sh[0, 1, :, off:off + n] = v.to(dev, torch.float32)
+        self.pool.write_pages_device(torch.tensor([page], dtype=torch.int32, device=dev), sh)
+        self.backend.synchronize()
+        if off + n == _lib.PAGE_SIZE:
+            self._shadow.pop(page, None)
+        else:
+            self._shadow[page] = sh
+        return n
 
     def _kv_np(self, t) -> np.ndarray:
         torch = _torch()
@@ -335,6 +388,10 @@ class HipBackend:
         if block is None or not block.is_valid():
             return                                   # backend.rs:296-298: no block, no store
         off = position % _lib.PAGE_SIZE
+        if self.pool.kv_format in (_lib.KV_FP8_E4M3, _lib.KV_MXFP8):
+            n = self._append_quantised(int(block), off, key, value)
+            self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + n)
+            return
         k = self._kv_np(key)
         v = self._kv_np(value)
         if k.shape[0] != self.pool.num_kv_heads or k.shape[2] != self.pool.head_dim:

@@ -29,7 +29,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-fno-honor-nans", "-mno-amdgpu-ieee"]
 HOST = ["-D__HIP_PLATFORM_AMD__", f"-I{os.path.join(ROCM, 'include')}", "-x", "c++"]
 
-HIP_SOURCES = ["decode_kernels.hip"]
+HIP_SOURCES = ["decode_kernels.hip", "write_kernels.hip"]
 HOST_SOURCES = ["api.cpp", "planner.cpp", "block_model.cpp", "synth.cpp"]
 
 

@@ -401,6 +401,22 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
     return st;
 }
 
+dh_status dh_pool_write_pages_device(dh_pool* p, const uint32_t* ids, uint32_t n, const void* src,
+                                     uint32_t src_dtype, void* stream) {
+    if (!p) return fail(DH_EINVAL, "pool is NULL");
+    if (n == 0) return DH_OK;
+    if (!ids || !src) return fail(DH_EINVAL, "NULL argument");
+    if (src_dtype > DH_DTYPE_F32) return fail(DH_EINVAL, "bad source dtype %u", src_dtype);
+    if (reinterpret_cast<uintptr_t>(src) & 15) return fail(DH_EINVAL, "src must be 16-byte aligned");
+    if (p->d != 64 && p->d != 128 && p->d != 256)
+        return fail(DH_EUNSUPPORTED, "head_dim %u: device page writes take 64, 128 or 256", p->d);
+    DH_DEVICE(p->be->device);
+    const hipError_t e = hipError_t(dh::launch_write_pages(ids, n, src, src_dtype, p->data, p->scales,
+                                                           p->num_pages, p->hkv, p->d, p->fmt, stream));
+    if (e != hipSuccess) return fail(DH_EHIP, "page write launch failed: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+
 dh_status dh_pool_copy_page(dh_pool* p, uint32_t src, uint32_t dst, void* stream) {
     if (!p) return fail(DH_EINVAL, "pool is NULL");
     if (src >= p->num_pages || dst >= p->num_pages)

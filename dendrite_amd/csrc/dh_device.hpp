@@ -116,9 +116,13 @@ DH_HOST_DEVICE inline uint64_t plane_offset(uint32_t page, uint32_t plane, uint3
 
 }  // namespace dh
 
-// Kernel launchers (defined in decode_kernels.hip).  Return hipError_t as int.
+// Kernel launchers (defined in decode_kernels.hip and write_kernels.hip).
+// Return hipError_t as int.
 extern "C++" {
 namespace dh {
+int launch_write_pages(const uint32_t* ids, uint32_t n, const void* src, uint32_t src_dtype, uint8_t* data,
+                       uint8_t* scales, uint32_t num_pages, uint32_t hkv, uint32_t d, uint32_t fmt,
+                       void* stream);
 int launch_attend(const AttendArgs& a, uint32_t n_tasks, uint32_t q_dtype, uint32_t kv_format,
                   uint32_t head_dim, void* stream);
 int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t head_dim, void* stream);

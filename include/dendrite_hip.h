@@ -175,6 +175,27 @@ dh_status dh_pool_write_tokens(dh_pool* pool, uint32_t page_id, uint32_t tok_off
  * page_ids[i] receives data[i] and scales[i] in the pool layout above. */
 dh_status dh_pool_write_pages(dh_pool* pool, const uint32_t* page_ids, uint32_t n,
                               const void* data, const void* scales, void* stream);
+/* Quantise-on-write from device memory: page_ids[i] (device uint32[n]) of
+ * the pool receives src[i] (device, 16-byte aligned,
+ * [n][2][num_kv_heads][16][head_dim] of src_dtype, DH_DTYPE_*: K plane then
+ * V plane; tokens past a partial page's length must be zero) in the pool's
+ * format:
+ *   F32 / BF16 / F16 : the value, converted with round to nearest even;
+ *   FP8_E4M3         : scale = amax / 448 per (page, K|V, kv head), 1 if
+ *                      amax = 0; element = E4M3 of x / scale, round to
+ *                      nearest even, saturated to +-448 (fp8.rs:39-52);
+ *   MXFP8            : per 32 consecutive elements along head_dim
+ *                      (quantization/mod.rs:96-97) scale = 2^(floor(log2
+ *                      amax) - 8) as E8M0 (2^-127 .. 2^127); element = E4M3
+ *                      of x / scale, saturated.
+ * Ids >= the pool size (INVALID included) are skipped: the ids live in device
+ * memory, so the host cannot check them.  The device half of
+ * ReferenceBackend::append_kv / store_kv (attention/backend.rs:285-301,
+ * 140-143) for K/V already in HBM; the reference has no FP8 codec
+ * (quantization/fp8.rs:29-53 states the ranges only).  Enqueued on `stream`;
+ * allocates nothing. */
+dh_status dh_pool_write_pages_device(dh_pool* pool, const uint32_t* page_ids, uint32_t n,
+                                     const void* src, uint32_t src_dtype, void* stream);
 /* Copy-on-write data copy src -> dst (all planes and scales).  The reference
  * leaves this as a TODO: crates/dendrite-core/src/cache/pool.rs:90. */
 dh_status dh_pool_copy_page(dh_pool* pool, uint32_t src, uint32_t dst, void* stream);

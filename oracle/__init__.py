@@ -63,6 +63,11 @@ def lib() -> C.CDLL:
         L.oracle_merge.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float,
                                    C.POINTER(C.c_float), C.POINTER(C.c_float)]
         L.oracle_num_threads.restype = C.c_int
+        L.oracle_e4m3_encode.restype = C.c_uint8
+        L.oracle_e4m3_encode.argtypes = [C.c_float]
+        L.oracle_write_pages.restype = C.c_int
+        L.oracle_write_pages.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32,
+                                         C.c_void_p, C.c_void_p]
         _lib = L
     return _lib
 
@@ -123,3 +128,26 @@ def decode(pool: PoolView, q, q_dtype, hq, scale, gqa, indptr, indices, last_pag
     if rc != 0:
         raise ValueError("oracle: a referenced page is absent from the pool view")
     return out
+
+
+def e4m3_encode(x: float) -> int:
+    """E4M3 code of a float: nearest finite value, ties to even, saturating."""
+    return lib().oracle_e4m3_encode(x)
+
+
+def scale_record_bytes(fmt: int, hkv: int, d: int) -> int:
+    return {FP8: 2 * hkv * 4, MX: 2 * hkv * 16 * (d // 32)}.get(fmt, 0)
+
+
+def write_pages(fmt: int, hkv: int, d: int, src: np.ndarray):
+    """The page write rule on float pages src [n][2][hkv][16][d]: returns
+    (data uint8 [n, page_bytes], scales uint8 [n, scale_bytes] or None)."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    n = src.shape[0]
+    eb = {F32: 4, BF16: 2, F16: 2, FP8: 1, MX: 1}[fmt]
+    data = np.zeros((n, 2 * hkv * 16 * d * eb), dtype=np.uint8)
+    sb = scale_record_bytes(fmt, hkv, d)
+    scales = np.zeros((n, max(sb, 1)), dtype=np.uint8)
+    rc = lib().oracle_write_pages(fmt, hkv, d, src.ctypes.data, n, data.ctypes.data, scales.ctypes.data)
+    assert rc == 0, "bad format"
+    return data, (scales if sb else None)

@@ -62,6 +62,120 @@ double oracle_e4m3(uint8_t b) {
 /* OCP MX E8M0: 2^(e - 127), e = 255 is NaN. */
 double oracle_e8m0(uint8_t e) { return e == 255 ? NAN : ldexp(1.0, (int)e - 127); }
 
+/* ------------------------------------------------ quantise-on-write oracle
+ * The page write rule (dh_pool_write_pages_device), restated from the format
+ * definitions: E4M3 "FN" encodes a float as the nearest finite code value
+ * (searched over the code table), ties to the even code, |x| >= 448
+ * saturating to +-448 (fp8.rs:39-52 states that range); block scales as the
+ * benchmark configurations define them: FP8 amax / 448 per (page, K|V, head),
+ * 1 for amax 0; MXFP8 2^(floor(log2 amax) - 8) per 32 along head_dim
+ * (quantization/mod.rs:96-97), as E8M0 clamped to 2^-127 .. 2^127. */
+double oracle_f16(uint16_t h);
+
+static double e4m3_tab[127];
+static int e4m3_tab_init = 0;
+
+uint8_t oracle_e4m3_encode(float x) {
+    if (!e4m3_tab_init) {
+        for (int c = 0; c < 127; ++c) e4m3_tab[c] = oracle_e4m3((uint8_t)c);
+        e4m3_tab_init = 1;
+    }
+    if (x != x) return 0x7F;
+    const uint8_t s = signbit(x) ? 0x80 : 0x00;
+    const double a = fabs((double)x);
+    if (a >= 448.0) return s | 0x7E;
+    int best = 0;
+    double bd = a;
+    for (int c = 1; c < 127; ++c) {
+        const double dd = fabs(e4m3_tab[c] - a);
+        if (dd < bd || (dd == bd && (c & 1) == 0)) {
+            best = c;
+            bd = dd;
+        }
+    }
+    return (uint8_t)(s | best);
+}
+
+/* Nearest bfloat16 (ties to the even pattern) of a finite float. */
+static uint16_t bf16_nearest(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t lo = u & 0xFFFF0000u, hi = lo + 0x10000u;
+    float flo, fhi;
+    memcpy(&flo, &lo, 4);
+    memcpy(&fhi, &hi, 4);
+    const double dl = fabs((double)x - flo), dh = fabs((double)fhi - x);
+    if (dl < dh || (dl == dh && ((lo >> 16) & 1) == 0)) return (uint16_t)(lo >> 16);
+    return (uint16_t)(hi >> 16);
+}
+
+/* Nearest IEEE half (ties to the even pattern; from 65520 on, infinity) of
+ * a finite float, by bisection over the ordered finite patterns. */
+static uint16_t f16_nearest(float x) {
+    const uint16_t s = signbit(x) ? 0x8000 : 0x0000;
+    const double a = fabs((double)x);
+    if (a >= 65520.0) return s | 0x7C00;
+    int lo = 0, hi = 0x7BFF;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (oracle_f16((uint16_t)mid) <= a) lo = mid;
+        else hi = mid - 1;
+    }
+    if (lo == 0x7BFF) return s | 0x7BFF;
+    const double dl = a - oracle_f16((uint16_t)lo), dh = oracle_f16((uint16_t)(lo + 1)) - a;
+    if (dl < dh || (dl == dh && (lo & 1) == 0)) return (uint16_t)(s | lo);
+    return (uint16_t)(s | (lo + 1));
+}
+
+/* src: n pages of [2][hkv][16][d] floats; data / scales: the pool records. */
+int oracle_write_pages(uint32_t fmt, uint32_t hkv, uint32_t d, const float* src, uint32_t n, uint8_t* data,
+                       uint8_t* scales) {
+    const size_t block = (size_t)OR_PAGE * d, nblk = (size_t)2 * hkv;
+    for (size_t i = 0; i < n; ++i) {
+        for (size_t b = 0; b < nblk; ++b) {
+            const float* x = src + (i * nblk + b) * block;
+            const size_t e0 = (i * nblk + b) * block;
+            if (fmt == F32) {
+                memcpy(data + e0 * 4, x, block * 4);
+            } else if (fmt == BF16) {
+                for (size_t e = 0; e < block; ++e) {
+                    const uint16_t h = bf16_nearest(x[e]);
+                    memcpy(data + (e0 + e) * 2, &h, 2);
+                }
+            } else if (fmt == F16) {
+                for (size_t e = 0; e < block; ++e) {
+                    const uint16_t h = f16_nearest(x[e]);
+                    memcpy(data + (e0 + e) * 2, &h, 2);
+                }
+            } else if (fmt == FP8) {
+                float amax = 0.f;
+                for (size_t e = 0; e < block; ++e) amax = fmaxf(amax, fabsf(x[e]));
+                const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+                for (size_t e = 0; e < block; ++e) data[e0 + e] = oracle_e4m3_encode(x[e] / sc);
+                memcpy(scales + (i * nblk + b) * 4, &sc, 4);
+            } else if (fmt == MX) {
+                for (size_t g = 0; g < block; g += 32) {
+                    float amax = 0.f;
+                    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(x[g + k]));
+                    int se = -127;
+                    if (amax > 0.f) {
+                        int ex;
+                        frexpf(amax, &ex);                 /* amax in [2^(ex-1), 2^ex) */
+                        se = ex - 1 - 8;
+                        se = se < -127 ? -127 : (se > 127 ? 127 : se);
+                    }
+                    scales[(i * nblk + b) * (block / 32) + g / 32] = (uint8_t)(se + 127);
+                    const float inv = ldexpf(1.0f, -se);
+                    for (int k = 0; k < 32; ++k) data[e0 + g + k] = oracle_e4m3_encode(x[g + k] * inv);
+                }
+            } else {
+                return -1;
+            }
+        }
+    }
+    return 0;
+}
+
 double oracle_bf16(uint16_t h) {
     uint32_t u = (uint32_t)h << 16;
     float f;
