@@ -13,18 +13,130 @@
 
 #include <algorithm>
 #include <unordered_map>
-#include <unordered_set>
 
 #include "dendrite_hip.h"
 
 namespace dh {
 namespace {
 
-struct TrieNode {
-    uint32_t page;
-    uint32_t count = 0;                 // sequences whose path passes here
-    uint32_t segment = UINT32_MAX;      // shared segment id (count >= 2)
-    std::unordered_map<uint32_t, uint32_t> children;
+// A sequence's page list: a view of the caller's CSR indices, or of a copy
+// with INVALID entries dropped.
+struct PageList {
+    const uint32_t* p = nullptr;
+    uint32_t n = 0;
+    size_t size() const { return n; }
+    bool empty() const { return n == 0; }
+    uint32_t operator[](size_t k) const { return p[k]; }
+    uint32_t back() const { return p[n - 1]; }
+    const uint32_t* data() const { return p; }
+    const uint32_t* begin() const { return p; }
+    const uint32_t* end() const { return p + n; }
+};
+
+// Compressed trie over block ids (a radix tree whose edges are runs of
+// pages): a node is a run seq_pages[src][off .. off + len) that `count`
+// sequences' page lists pass through.  Inserting a list compares whole runs
+// and splits a node only where lists diverge or end, so once every list is
+// in, the nodes reached by >= 2 lists are exactly the maximal runs shared
+// by the same set of sequences: the shared segments.  A node's first child
+// is kept inline; further children (forks) go to one map keyed by
+// (node, first page).
+struct RunNode {
+    uint32_t src = 0, off = 0, len = 0;
+    uint32_t count = 0;
+    uint32_t segment = UINT32_MAX;
+    uint32_t first_page = DH_INVALID_PAGE;   // first page of the inline child
+    uint32_t first_child = 0;
+    uint32_t nchildren = 0;
+};
+
+struct RunTrie {
+    const std::vector<PageList>& lists;
+    std::vector<RunNode> nodes;
+    std::unordered_map<uint64_t, uint32_t> more;
+
+    RunTrie(const std::vector<PageList>& l, size_t max_nodes) : lists(l) {
+        nodes.reserve(max_nodes);
+        nodes.emplace_back();   // root: the empty run
+    }
+    uint32_t page(const RunNode& n, uint32_t k) const { return lists[n.src][n.off + k]; }
+    static uint64_t key(uint32_t node, uint32_t pg) { return (uint64_t(node) << 32) | pg; }
+
+    uint32_t child(uint32_t cur, uint32_t pg) const {
+        const RunNode& n = nodes[cur];
+        if (n.nchildren && n.first_page == pg) return n.first_child;
+        if (n.nchildren > 1) {
+            const auto it = more.find(key(cur, pg));
+            if (it != more.end()) return it->second;
+        }
+        return UINT32_MAX;
+    }
+    void set_child(uint32_t cur, uint32_t pg, uint32_t c, bool added) {
+        RunNode& n = nodes[cur];
+        if (n.nchildren == 0 || n.first_page == pg) {
+            n.first_page = pg;
+            n.first_child = c;
+        } else {
+            more[key(cur, pg)] = c;
+        }
+        if (added) n.nchildren++;
+    }
+
+    // Inserts the first n pages of sequence b's list.
+    void insert(uint32_t b, size_t n) {
+        const PageList& pl = lists[b];
+        uint32_t cur = 0;
+        size_t i = 0;
+        while (i < n) {
+            uint32_t c = child(cur, pl[i]);
+            if (c == UINT32_MAX) {
+                c = uint32_t(nodes.size());
+                nodes.emplace_back();
+                nodes[c].src = b;
+                nodes[c].off = uint32_t(i);
+                nodes[c].len = uint32_t(n - i);
+                nodes[c].count = 1;
+                set_child(cur, pl[i], c, true);
+                return;
+            }
+            const uint32_t lim = uint32_t(std::min<size_t>(nodes[c].len, n - i));
+            uint32_t m = 1;
+            while (m < lim && page(nodes[c], m) == pl[i + m]) ++m;
+            if (m < nodes[c].len) {   // split c: its first m pages become a new parent x
+                const uint32_t x = uint32_t(nodes.size());
+                nodes.emplace_back();
+                RunNode& xn = nodes[x];
+                RunNode& cn = nodes[c];
+                xn.src = cn.src;
+                xn.off = cn.off;
+                xn.len = m;
+                xn.count = cn.count;
+                cn.off += m;
+                cn.len -= m;
+                xn.first_page = page(cn, 0);
+                xn.first_child = c;
+                xn.nchildren = 1;
+                set_child(cur, pl[i], x, false);
+                c = x;
+            }
+            nodes[c].count++;
+            cur = c;
+            i += m;
+        }
+    }
+
+    // The nodes the first n pages of an inserted list pass through, in
+    // order (after every insertion: a later split moves a node's front into
+    // a new parent).
+    void path(uint32_t b, size_t n, std::vector<uint32_t>& out) const {
+        const PageList& pl = lists[b];
+        uint32_t cur = 0;
+        for (size_t i = 0; i < n;) {
+            cur = child(cur, pl[i]);
+            out.push_back(cur);
+            i += nodes[cur].len;
+        }
+    }
 };
 
 struct Segment {
@@ -52,8 +164,11 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     const uint32_t r = in.hq / in.hkv;
 
     // 1. Page lists with INVALID entries dropped (ReferenceBackend::decode
-    //    skips blocks it has no KV for, attention/backend.rs:228-233).
-    std::vector<std::vector<uint32_t>> seq_pages(B);
+    //    skips blocks it has no KV for, attention/backend.rs:228-233): views
+    //    of the indices, or of a filtered copy when there are INVALID ids.
+    std::vector<PageList> seq_pages(B);
+    std::vector<uint32_t> kept;
+    bool any_invalid = false;
     for (uint32_t b = 0; b < B; ++b) {
         if (in.indptr[b + 1] < in.indptr[b]) {
             err = "indptr must be non-decreasing";
@@ -61,14 +176,30 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         }
         for (uint32_t k = in.indptr[b]; k < in.indptr[b + 1]; ++k) {
             const uint32_t p = in.indices[k];
-            if (p == DH_INVALID_PAGE) continue;
+            if (p == DH_INVALID_PAGE) {
+                any_invalid = true;
+                continue;
+            }
             if (p >= in.num_pool_pages) {
                 err = "page id " + std::to_string(p) + " outside the pool of " +
                       std::to_string(in.num_pool_pages) + " pages (sequence " +
                       std::to_string(b) + ")";
                 return DH_EINVAL;
             }
-            seq_pages[b].push_back(p);
+        }
+    }
+    if (any_invalid) {
+        kept.reserve(in.indptr[B]);
+        for (uint32_t k = 0; k < in.indptr[B]; ++k)
+            if (in.indices[k] != DH_INVALID_PAGE) kept.push_back(in.indices[k]);
+    }
+    for (uint32_t b = 0, o = 0; b < B; ++b) {
+        if (any_invalid) {
+            const uint32_t o0 = o;
+            for (uint32_t k = in.indptr[b]; k < in.indptr[b + 1]; ++k) o += in.indices[k] != DH_INVALID_PAGE;
+            seq_pages[b] = PageList{kept.data() + o0, o - o0};
+        } else {
+            seq_pages[b] = PageList{in.indices + in.indptr[b], in.indptr[b + 1] - in.indptr[b]};
         }
         if (uint64_t(seq_pages[b].size()) * kPageSize > DH_MAX_SEQ_LEN) {
             err = "sequence " + std::to_string(b) + " exceeds MAX_SEQ_LEN";
@@ -82,65 +213,38 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     std::vector<std::vector<uint32_t>> seq_segs(B);   // segment ids per sequence
     std::vector<std::vector<uint32_t>> private_pages(B);
     if (in.cascade) {
-        std::vector<TrieNode> nodes(1);
-        nodes[0].page = DH_INVALID_PAGE;
+        // Every list but its last page (only a sequence's last page may be
+        // partial, so it stays private).  Each insertion adds at most two nodes.
+        RunTrie trie(seq_pages, 2 * size_t(B) + 1);
         std::vector<std::vector<uint32_t>> paths(B);
+        for (uint32_t b = 0; b < B; ++b)
+            if (seq_pages[b].size() > 1) trie.insert(b, seq_pages[b].size() - 1);
+        for (uint32_t b = 0; b < B; ++b)
+            if (seq_pages[b].size() > 1) trie.path(b, seq_pages[b].size() - 1, paths[b]);
+        // Shared nodes become segments in order of first use; a list's nodes
+        // reached by it alone (all after its last shared one) and its last
+        // page are its private pages.
         for (uint32_t b = 0; b < B; ++b) {
-            const auto& pl = seq_pages[b];
-            uint32_t cur = 0;
-            for (size_t k = 0; k + 1 < pl.size(); ++k) {
-                auto it = nodes[cur].children.find(pl[k]);
-                uint32_t nxt;
-                if (it == nodes[cur].children.end()) {
-                    nxt = uint32_t(nodes.size());
-                    nodes[cur].children.emplace(pl[k], nxt);
-                    nodes.emplace_back();
-                    nodes.back().page = pl[k];
-                } else {
-                    nxt = it->second;
-                }
-                nodes[nxt].count++;
-                paths[b].push_back(nxt);
-                cur = nxt;
-            }
-        }
-        // A shared segment is a maximal chain of nodes with count >= 2 where
-        // each node is the only child of the previous one and keeps its count
-        // (so the chain is referenced by exactly the same sequences).
-        for (uint32_t b = 0; b < B; ++b) {
-            const auto& path = paths[b];
-            uint32_t prev = 0;
-            for (size_t k = 0; k < path.size(); ++k) {
-                const uint32_t u = path[k];
-                TrieNode& n = nodes[u];
+            for (const uint32_t u : paths[b]) {
+                RunNode& n = trie.nodes[u];
+                const uint32_t* run = seq_pages[n.src].data() + n.off;
                 if (n.count < 2) {
-                    private_pages[b].push_back(n.page);
-                } else {
-                    if (n.segment == UINT32_MAX) {
-                        const bool extend = prev != 0 && nodes[prev].count == n.count &&
-                                            nodes[prev].children.size() == 1 &&
-                                            nodes[prev].segment != UINT32_MAX;
-                        if (extend) {
-                            n.segment = nodes[prev].segment;
-                            segs[n.segment].pages.push_back(n.page);
-                        } else {
-                            n.segment = uint32_t(segs.size());
-                            segs.emplace_back();
-                            segs.back().pages.push_back(n.page);
-                        }
-                    }
-                    if (seq_segs[b].empty() || seq_segs[b].back() != n.segment) {
-                        seq_segs[b].push_back(n.segment);
-                        segs[n.segment].seqs.push_back(b);
-                    }
+                    private_pages[b].insert(private_pages[b].end(), run, run + n.len);
+                    continue;
                 }
-                prev = u;
+                if (n.segment == UINT32_MAX) {
+                    n.segment = uint32_t(segs.size());
+                    segs.emplace_back();
+                    segs.back().pages.assign(run, run + n.len);
+                }
+                seq_segs[b].push_back(n.segment);
+                segs[n.segment].seqs.push_back(b);
             }
             if (!seq_pages[b].empty()) private_pages[b].push_back(seq_pages[b].back());
         }
         out.num_shared_segments = uint32_t(segs.size());
     } else {
-        for (uint32_t b = 0; b < B; ++b) private_pages[b] = seq_pages[b];
+        for (uint32_t b = 0; b < B; ++b) private_pages[b].assign(seq_pages[b].begin(), seq_pages[b].end());
     }
     for (uint32_t b = 0; b < B; ++b) {
         if (private_pages[b].empty()) continue;
@@ -218,14 +322,20 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     // 5. Items.  Group items that read the same pages are kept together.
     std::vector<Group> groups;      // group items by (segment, chunk, head)
     std::vector<std::pair<double, Item>> waves;
-    std::unordered_set<uint32_t> uniq;
+    // Distinct pages of the plan, for the statistics: a bitmap over the pool.
+    std::vector<uint64_t> seen((uint64_t(in.num_pool_pages) + 63) / 64, 0);
+    uint64_t uniq = 0;
     for (size_t s = 0; s < segs.size(); ++s) {
         const Segment& sg = segs[s];
         const bool grp = is_group(sg);
         const uint32_t np = uint32_t(sg.pages.size());
         const uint32_t base = uint32_t(out.pages.size());
         out.pages.insert(out.pages.end(), sg.pages.begin(), sg.pages.end());
-        for (uint32_t p : sg.pages) uniq.insert(p);
+        for (uint32_t p : sg.pages) {
+            const uint64_t bit = 1ull << (p & 63);
+            uniq += (seen[p >> 6] & bit) == 0;
+            seen[p >> 6] |= bit;
+        }
         out.page_reads += np;
         const uint32_t nc = nchunks[s];
         const uint32_t rows = uint32_t(sg.seqs.size()) * r;
@@ -260,7 +370,7 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
             }
         }
     }
-    out.unique_pages = uniq.size();
+    out.unique_pages = uniq;
 
     // 6. Tasks.  Heaviest first.  Group tasks that read the same pages land
     //    on the same XCD (workgroups are dispatched round-robin over the 8
