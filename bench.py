@@ -101,6 +101,64 @@ def measured_traffic(workload: str):
     return t.get("hbm_bytes_per_launch")
 
 
+def bench_prefill(args):
+    """Paged causal prefill: B sequences of CTX cached + NEW query tokens in
+    shuffled pool pages; q / out [B*NEW, Hq, D] resident in HBM.  The work
+    is MFMA-bound: flops = 4 Hq D sum over queries of the tokens each sees
+    (QK and PV products); the roofline peak is the dense MFMA rate of the
+    compute dtype."""
+    import torch
+    from dendrite_amd import workloads
+    from dendrite_amd.backend import Backend, Pool, PrefillPlan, decode_batch
+    spec, _, nb = args.prefill.partition("x")
+    ctx, new = (int(x) for x in spec.split(":"))
+    B = int(nb) if nb else 1
+    w = workloads.ALL[args.workload]()
+    kv = ctx + new
+    npg = (kv + 15) // 16
+    pool_pages = B * npg
+    be = Backend(0)
+    pool = Pool(be, pool_pages, w.hkv, w.d, w.kv_format)
+    perm = np.random.default_rng(1).permutation(pool_pages).astype(np.uint32)
+    ids = np.arange(pool_pages, dtype=np.uint32)
+    for c0 in range(0, pool_pages, 8192):
+        data, scales = w.make_pages(ids[c0:c0 + 8192])
+        pool.write_pages(ids[c0:c0 + 8192], data, scales)
+    indptr = np.arange(B + 1, dtype=np.uint32) * npg
+    plan = PrefillPlan(be, w.attention_config(), pool, indptr, perm, np.full(B, kv, np.uint32),
+                       np.full(B, new, np.uint32), causal=True)
+    dt = torch.bfloat16 if w.q_dtype == 1 else torch.float16
+    q = torch.randn((B * new, w.hq, w.d), device="cuda").to(dt)
+    out = torch.empty_like(q)
+    ws = plan.workspace()
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        decode_batch(plan, q, out, ws, stream=stream)
+    torch.cuda.synchronize()
+    res = {}
+    for stages in (3, 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            decode_batch(plan, q, out, ws, stream=stream, stages=stages)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[stages] = e0.elapsed_time(e1) * 1e3 / args.steps
+    seen = B * (new * ctx + new * (new + 1) // 2)
+    flops = 4.0 * w.hq * w.d * seen
+    tf = flops / (res[3] * 1e-6) / 1e12
+    tf_att = flops / (res[1] * 1e-6) / 1e12
+    peak = 2500.0   # dense bf16 / f16 MFMA, TFLOP/s
+    print(json.dumps({"metric": "paged causal prefill throughput", "value": round(tf, 2), "unit": "TFLOP/s",
+                      "us_per_call": round(res[3], 2), "tokens_per_s": round(B * new / (res[3] * 1e-6), 1),
+                      "roofline": {"bound": "mfma", "achieved": round(tf_att, 2), "peak": peak, "unit": "TFLOP/s",
+                                   "frac": round(tf_att / peak, 4), "attention_us": round(res[1], 2)},
+                      "config": {"workload": w.name, "num_heads": w.hq, "num_kv_heads": w.hkv, "head_dim": w.d,
+                                 "kv_format": w.kv_format, "context": ctx, "new_tokens": new, "sequences": B,
+                                 "plan_items": plan.stats()["num_items"], "flops": flops},
+                      "steps": args.steps, "warmup": args.warmup}), flush=True)
+
+
 def bench_write(args):
     """Quantise-on-write throughput: N bf16 pages [2][Hkv][16][D] resident in
     HBM into a pool of the workload's shape and format, through
@@ -148,6 +206,9 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--prefill", default="", metavar="CTX:NEW[xB]",
+                    help="only measure paged causal prefill: NEW query tokens after CTX cached tokens, "
+                         "B sequences, at the workload's head shape and KV format (e.g. 0:4096, 8192:2048x4)")
     ap.add_argument("--write-pages", type=int, default=0, metavar="N",
                     help="only measure quantise-on-write (dh_pool_write_pages_device) of N bf16 pages "
                          "into a pool of the workload's shape and KV format")
@@ -177,6 +238,9 @@ def main():
 
     if args.write_pages:
         bench_write(args)
+        return
+    if args.prefill:
+        bench_prefill(args)
         return
 
     ws_list = build_workloads(args.workload, args.rotations)

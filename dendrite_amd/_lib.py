@@ -108,6 +108,8 @@ SIGNATURES = {
     "dh_pool_read_page": (_I, [_P, _U32, _P, _P]),
     "dh_plan_create": (_I, [_P, C.POINTER(dh_attn_config), _P, _PU32, _PU32, _U32, _U32,
                             C.POINTER(dh_plan_options), C.POINTER(_P)]),
+    "dh_plan_create_prefill": (_I, [_P, C.POINTER(dh_attn_config), _P, _PU32, _PU32, _PU32, _PU32, _U32, _U32,
+                                    _U32, C.POINTER(_P)]),
     "dh_plan_destroy": (_I, [_P]),
     "dh_plan_workspace_size": (C.c_size_t, [_P]),
     "dh_plan_get_stats": (_I, [_P, C.POINTER(dh_plan_stats)]),

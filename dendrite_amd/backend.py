@@ -307,6 +307,32 @@ def plan_inspect(config: AttentionConfig, num_pool_pages: int, indptr, indices, 
             "pages": pages[:npg.value], "seqslots": ss[:2 * nss.value].reshape(-1, 2)}
 
 
+class PrefillPlan(DecodePlan):
+    """dh_plan_create_prefill: attention of each sequence's last q_len tokens
+    over its kv_len paged tokens, causal (bottom-right aligned) or full; run
+    with decode_batch on q / out of [sum(q_len), num_heads, head_dim]."""
+
+    def __init__(self, backend: Backend, config: AttentionConfig, pool: Pool, indptr, indices, kv_len, q_len,
+                 causal: bool = True, chunk_pages: int = 0):
+        self.backend = backend
+        self.pool = pool
+        self.config = config
+        ip = np.ascontiguousarray(indptr, dtype=np.uint32)
+        ix = np.ascontiguousarray(indices, dtype=np.uint32)
+        kv = np.ascontiguousarray(kv_len, dtype=np.uint32)
+        ql = np.ascontiguousarray(q_len, dtype=np.uint32)
+        self.batch_size = len(ip) - 1
+        self.num_queries = int(ql.sum())
+        self._c = config.to_c()
+        self._h = C.c_void_p()
+        self._destroy = lib().dh_plan_destroy
+        check(lib().dh_plan_create_prefill(backend._h, C.byref(self._c), pool._h, ip.ctypes.data_as(_lib._PU32),
+                                           ix.ctypes.data_as(_lib._PU32) if len(ix) else None,
+                                           kv.ctypes.data_as(_lib._PU32), ql.ctypes.data_as(_lib._PU32),
+                                           self.batch_size, int(causal), chunk_pages, C.byref(self._h)))
+        self.workspace_size = lib().dh_plan_workspace_size(self._h)
+
+
 def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream=None,
                  stages: int = 3) -> None:
     """One decode step through dh_decode_stages (stages=3 is dh_decode_batch).
@@ -445,8 +471,45 @@ class HipBackend:
         return self.decode_batch([query], [block_table], config)[0]
 
     def prefill(self, query, key, value, block_table: BlockTable, config: AttentionConfig):
-        raise DhError(_lib.DH_EUNSUPPORTED, "prefill is not implemented on the HIP backend")
+        """ReferenceBackend::prefill (backend.rs:163-204): causal attention of
+        query [B, num_heads, S, head_dim] over key / value [B, num_kv_heads,
+        S, head_dim] (GQA per config), output like query.  As there, the block
+        table is not read: K / V are staged in a temporary pool of the query's
+        dtype and run through a prefill plan (q_len = kv_len = S)."""
+        torch = _torch()
+        dev = f"cuda:{self.backend.device}"
+        if query.dtype not in (torch.bfloat16, torch.float16):
+            raise DhError(_lib.DH_EUNSUPPORTED, "prefill takes bf16 or f16 queries")
+        bsz, hq, S, d = query.shape
+        hkv = key.shape[1]
+        if tuple(key.shape) != (bsz, hkv, S, d) or tuple(value.shape) != tuple(key.shape):
+            raise DhError(_lib.DH_EINVAL, f"key / value shape {tuple(key.shape)} does not match the query")
+        if S == 0 or bsz == 0:
+            return torch.zeros_like(query)
+        npg = (S + _lib.PAGE_SIZE - 1) // _lib.PAGE_SIZE
+        fmt = _lib.KV_BF16 if query.dtype == torch.bfloat16 else _lib.KV_F16
+        pool = Pool(self.backend, bsz * npg, hkv, d, fmt)
+        pad = npg * _lib.PAGE_SIZE - S
+        kv = torch.stack([key, value], dim=1).to(dev, query.dtype)            # [B, 2, Hkv, S, D]
+        kv = torch.nn.functional.pad(kv, (0, 0, 0, pad))                       # [B, 2, Hkv, npg*16, D]
+        src = kv.reshape(bsz, 2, hkv, npg, _lib.PAGE_SIZE, d).permute(0, 3, 1, 2, 4, 5).contiguous()
+        src = src.reshape(bsz * npg, 2, hkv, _lib.PAGE_SIZE, d)
+        pool.write_pages_device(torch.arange(bsz * npg, dtype=torch.int32, device=dev), src)
+        cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
+        cfg.scale = config.scale
+        cfg.gqa_mapping = config.gqa_mapping
+        cfg.q_dtype = dtype_code(query.dtype)
+        cfg.kv_format = fmt
+        indptr = np.arange(bsz + 1, dtype=np.uint32) * npg
+        indices = np.arange(bsz * npg, dtype=np.uint32)
+        lens = np.full(bsz, S, dtype=np.uint32)
+        plan = PrefillPlan(self.backend, cfg, pool, indptr, indices, lens, lens, causal=True)
+        q = query.to(dev).permute(0, 2, 1, 3).reshape(bsz * S, hq, d).contiguous()
+        out = torch.empty_like(q)
+        decode_batch(plan, q, out, plan.workspace())
+        torch.cuda.synchronize(dev)
+        return out.reshape(bsz, S, hq, d).permute(0, 2, 1, 3).contiguous()
 
 
-__all__ = ["AttentionConfig", "Backend", "Pool", "DecodePlan", "decode_batch", "HipBackend",
+__all__ = ["AttentionConfig", "Backend", "Pool", "DecodePlan", "PrefillPlan", "decode_batch", "HipBackend",
            "is_available", "dtype_code", "torch_dtype", "raw_to_tensor"]

@@ -125,6 +125,10 @@ struct dh_plan {
     uint32_t* pages;
     dh::SeqSlot* seqslots;
     uint32_t* slot_ptr;
+    // Prefill plans: tokens each query sees, item token ranges.
+    bool prefill;
+    uint32_t* row_len;
+    dh::ItemLim* item_lim;
     dh_plan_stats stats;
     size_t ws_bytes;
     size_t ws_lse_off;
@@ -526,19 +530,10 @@ dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages, co
     return DH_OK;
 }
 
-dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
-                         const uint32_t* indptr, const uint32_t* indices, uint32_t batch,
-                         uint32_t flags, const dh_plan_options* opt, dh_plan** out) {
-    if (!be || !pool || !out || !cfg) return fail(DH_EINVAL, "NULL argument");
-    *out = nullptr;
-    if (pool->hkv != cfg->num_kv_heads || pool->d != cfg->head_dim || pool->fmt != cfg->kv_format)
-        return fail(DH_EINVAL, "pool (kv heads %u, head_dim %u, format %u) does not match the config "
-                    "(%u, %u, %u)", pool->hkv, pool->d, pool->fmt, cfg->num_kv_heads, cfg->head_dim,
-                    cfg->kv_format);
-    dh::HostPlan hp;
-    dh_status st = host_plan(cfg, pool->num_pages, indptr, indices, batch, flags, opt, hp);
-    if (st != DH_OK) return st;
-
+// Uploads a host plan: items, pages, seqslots, slot_ptr (and, for prefill,
+// per-query token counts and item token ranges) in one device blob.
+static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                             const dh::HostPlan& hp, uint32_t batch, bool prefill, dh_plan** out) {
     dh_plan* pl = new (std::nothrow) dh_plan;
     if (!pl) return fail(DH_ENOMEM, "out of host memory");
     memset(pl, 0, sizeof *pl);
@@ -551,16 +546,22 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     pl->n_group_items = hp.num_group_items;
     pl->n_wave_items = hp.num_wave_items;
     pl->n_slots = hp.num_slots;
+    pl->prefill = prefill;
     const size_t o_items = 0;
     const size_t o_pages = align_up(o_items + hp.items.size() * sizeof(dh::Item), 256);
     const size_t o_ss = align_up(o_pages + hp.pages.size() * sizeof(uint32_t), 256);
     const size_t o_sp = align_up(o_ss + hp.seqslots.size() * sizeof(dh::SeqSlot), 256);
-    const size_t total = align_up(o_sp + hp.slot_ptr.size() * sizeof(uint32_t), 256);
+    const size_t o_rl = align_up(o_sp + hp.slot_ptr.size() * sizeof(uint32_t), 256);
+    const size_t o_il = align_up(o_rl + hp.row_len.size() * sizeof(uint32_t), 256);
+    const size_t total = align_up(o_il + hp.item_lim.size() * sizeof(dh::ItemLim), 256);
     std::vector<uint8_t> blob(total, 0);
     memcpy(blob.data() + o_items, hp.items.data(), hp.items.size() * sizeof(dh::Item));
     memcpy(blob.data() + o_pages, hp.pages.data(), hp.pages.size() * sizeof(uint32_t));
     memcpy(blob.data() + o_ss, hp.seqslots.data(), hp.seqslots.size() * sizeof(dh::SeqSlot));
     memcpy(blob.data() + o_sp, hp.slot_ptr.data(), hp.slot_ptr.size() * sizeof(uint32_t));
+    if (!hp.row_len.empty()) memcpy(blob.data() + o_rl, hp.row_len.data(), hp.row_len.size() * sizeof(uint32_t));
+    if (!hp.item_lim.empty())
+        memcpy(blob.data() + o_il, hp.item_lim.data(), hp.item_lim.size() * sizeof(dh::ItemLim));
     dh::DeviceGuard guard(be->device);
     hipError_t e = guard.error();
     if (e == hipSuccess) e = hipMalloc(&pl->dev, total);
@@ -575,6 +576,8 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     pl->pages = reinterpret_cast<uint32_t*>(pl->dev + o_pages);
     pl->seqslots = reinterpret_cast<dh::SeqSlot*>(pl->dev + o_ss);
     pl->slot_ptr = reinterpret_cast<uint32_t*>(pl->dev + o_sp);
+    pl->row_len = prefill ? reinterpret_cast<uint32_t*>(pl->dev + o_rl) : nullptr;
+    pl->item_lim = prefill ? reinterpret_cast<dh::ItemLim*>(pl->dev + o_il) : nullptr;
     const size_t rows = size_t(hp.num_slots) * cfg->num_heads;
     // Partial O: fp32 for f32 q, else f16 scaled per row (dh::PartialLse).
     const size_t o_bytes = cfg->q_dtype == DH_DTYPE_F32 ? sizeof(float) : sizeof(uint16_t);
@@ -584,6 +587,62 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     retain(be);
     *out = pl;
     return DH_OK;
+}
+
+static dh_status check_pool_matches(const dh_attn_config* cfg, const dh_pool* pool) {
+    if (pool->hkv != cfg->num_kv_heads || pool->d != cfg->head_dim || pool->fmt != cfg->kv_format)
+        return fail(DH_EINVAL, "pool (kv heads %u, head_dim %u, format %u) does not match the config "
+                    "(%u, %u, %u)", pool->hkv, pool->d, pool->fmt, cfg->num_kv_heads, cfg->head_dim,
+                    cfg->kv_format);
+    return DH_OK;
+}
+
+dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                         const uint32_t* indptr, const uint32_t* indices, uint32_t batch,
+                         uint32_t flags, const dh_plan_options* opt, dh_plan** out) {
+    if (!be || !pool || !out || !cfg) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    dh_status st = check_pool_matches(cfg, pool);
+    if (st != DH_OK) return st;
+    dh::HostPlan hp;
+    st = host_plan(cfg, pool->num_pages, indptr, indices, batch, flags, opt, hp);
+    if (st != DH_OK) return st;
+    return upload_plan(be, cfg, pool, hp, batch, false, out);
+}
+
+dh_status dh_plan_create_prefill(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                                 const uint32_t* indptr, const uint32_t* indices, const uint32_t* kv_len,
+                                 const uint32_t* q_len, uint32_t batch, uint32_t causal, uint32_t chunk_pages,
+                                 dh_plan** out) {
+    if (!be || !pool || !out || !cfg) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    dh_status st = validate_config(cfg);
+    if (st != DH_OK) return st;
+    st = check_pool_matches(cfg, pool);
+    if (st != DH_OK) return st;
+    const bool fp8 = cfg->kv_format == DH_KV_FP8_E4M3 || cfg->kv_format == DH_KV_MXFP8;
+    if (cfg->q_dtype == DH_DTYPE_F32 || (fp8 && cfg->head_dim == 64))
+        return fail(DH_EUNSUPPORTED, "prefill takes bf16 / f16 queries, and FP8 / MXFP8 KV at head_dim 128 or 256");
+    if (batch && (!indptr || !kv_len || !q_len)) return fail(DH_EINVAL, "NULL argument");
+    if (batch && indptr[batch] > indptr[0] && !indices) return fail(DH_EINVAL, "indices is NULL");
+    dh::PrefillInput in;
+    in.batch = batch;
+    static const uint32_t zero_ptr[1] = {0};
+    in.indptr = batch ? indptr : zero_ptr;
+    in.indices = indices;
+    in.kv_len = kv_len;
+    in.q_len = q_len;
+    in.num_pool_pages = pool->num_pages;
+    in.hq = cfg->num_heads;
+    in.hkv = cfg->num_kv_heads;
+    in.group_rows = uint32_t(dh::group_rows(false, int(cfg->head_dim)));
+    in.causal = causal != 0;
+    in.chunk_pages = chunk_pages;
+    dh::HostPlan hp;
+    std::string err;
+    const int rc = dh::build_prefill_plan(in, hp, err);
+    if (rc != DH_OK) return fail(dh_status(rc), "%s", err.c_str());
+    return upload_plan(be, cfg, pool, hp, uint32_t(hp.row_len.size()), true, out);
 }
 
 dh_status dh_plan_destroy(dh_plan* pl) {
@@ -654,7 +713,10 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         a.q_sign = sl < 0.f ? (c.q_dtype == DH_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
         a.n_group_items = pl->n_group_items;
         a.n_wave_items = pl->n_wave_items;
-        hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim, stream));
+        a.row_len = pl->row_len;
+        a.item_lim = pl->item_lim;
+        hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim,
+                                                    pl->prefill, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     }
     if (mask & 2u) {

@@ -1201,6 +1201,48 @@ __device__ __forceinline__ void dma_v_operands(uint32_t s, const LdsBases<D>& lb
     }
 }
 
+// Token masks of a page pair: s0[rt] / s1[rt] tokens of the two pages are
+// visible to the lane's row of tile rt (scores of the others are masked),
+// v0 / v1 tokens hold data (V past them is zeroed, so garbage past a
+// sequence's last token cannot reach O through a zero weight).
+template <int RT>
+struct PairMask {
+    int s0[RT], s1[RT];
+    int v0, v1;
+};
+
+template <int RT>
+__device__ __forceinline__ PairMask<RT> uniform_mask(int n0, int n1) {
+    PairMask<RT> m;
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m.s0[rt] = n0;
+        m.s1[rt] = n1;
+    }
+    m.v0 = n0;
+    m.v1 = n1;
+    return m;
+}
+
+// Masks of the pair starting at token t of a causal item: row tile rt sees
+// lenr[rt] tokens of the sequence, of which the item holds those below lmax
+// (rows of a chunk before the last see past its end: the cap keeps a
+// missing second page of the item's last pair masked).
+template <int RT>
+__device__ __forceinline__ PairMask<RT> causal_mask(int t, const uint32_t (&lenr)[RT], int lmax) {
+    auto cl = [](int x) { return min(max(x, 0), kPageSize); };
+    PairMask<RT> m;
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int len = min(int(lenr[rt]), lmax);
+        m.s0[rt] = cl(len - t);
+        m.s1[rt] = cl(len - t - kPageSize);
+    }
+    m.v0 = cl(lmax - t);
+    m.v1 = cl(lmax - t - kPageSize);
+    return m;
+}
+
 // One step of the pair loop after its barrier: the lazy-max check of pair
 // p (scores already in sc) and its rare rescale, then the LDS reads (V of
 // pair p from the slot at offset vs and, when NEXT, K of pair p + 1 from the
@@ -1209,7 +1251,8 @@ __device__ __forceinline__ void dma_v_operands(uint32_t s, const LdsBases<D>& lb
 // last pair only); the last pair has no next pair (NEXT false).  KS: the
 // pages' K scales ks0, ks1 multiply the scores (K was staged unscaled).
 template <int D, bool F16, int NRT, bool PART, bool NEXT, bool KS = false>
-__device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, int n0, int n1, const LdsBases<D>& lb,
+__device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMask<DmaCfg<D>::RT>& pm,
+                                         const LdsBases<D>& lb,
                                          const u32x4 (&qB)[DmaCfg<D>::RT][D / 32], f4 (&sc)[DmaCfg<D>::RT][2],
                                          u32x4 (&vop)[D / 16], RowMax<DmaCfg<D>::RT>& rm,
                                          f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], int g,
@@ -1219,8 +1262,8 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, int n0, int n
     float lm[RT];
     #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-        if constexpr (KS) lm[rt] = dma_lane_max_ks<RT, PART>(sc, rt, n0, n1, g, ks0, ks1);
-        else lm[rt] = dma_lane_max<RT, PART>(sc, rt, n0, n1, g);
+        if constexpr (KS) lm[rt] = dma_lane_max_ks<RT, PART>(sc, rt, pm.s0[rt], pm.s1[rt], g, ks0, ks1);
+        else lm[rt] = dma_lane_max<RT, PART>(sc, rt, pm.s0[rt], pm.s1[rt], g);
         need |= lm[rt] > rm.thr[rt];
     }
     if (__ballot(need)) dma_rescale<D, NRT>(lm, rm, Lsum, O, f, finv);
@@ -1233,8 +1276,8 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, int n0, int n
     if constexpr (PART) {
         #pragma unroll
         for (int e = 0; e < D / 16; ++e) {
-            mask_v_tr(vop[e], 0, g, n0);
-            mask_v_tr(vop[e], 2, g, n1);
+            mask_v_tr(vop[e], 0, g, pm.v0);
+            mask_v_tr(vop[e], 2, g, pm.v1);
         }
     }
     u32x4 kop[2][KB];
@@ -1282,6 +1325,7 @@ template <int RT>
 struct RowTargets {
     uint32_t qoff[RT];
     uint32_t dst[RT];
+    uint32_t len[RT];    // tokens the row sees (causal items only)
 };
 
 template <int D, int RT>
@@ -1295,13 +1339,15 @@ __device__ __forceinline__ void dma_row_targets(const AttendArgs& a, const Item&
         row_target(a, it, row, seq, slot, qh);
         rtg.qoff[rt] = (seq * a.hq + qh) * uint32_t(D * 2);
         rtg.dst[rt] = slot * a.hq + qh;
+        rtg.len[rt] = (it.flags & kItemCausal) ? a.row_len[seq] : 0u;
     }
 }
 
-template <int D, bool F16, int NRT, bool TAIL>
+template <int D, bool F16, int NRT, bool TAIL, bool CAUSAL>
 __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                uint8_t* ring, int tid, int wave, int g, int c,
                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
+                                               const ItemLim& lim,
                                                u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
                                                RowMax<DmaCfg<D>::RT>& rm, f4 (&Lsum)[DmaCfg<D>::RT],
                                                f4 (&O)[DmaCfg<D>::RT][D / 16]) {
@@ -1395,9 +1441,19 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
                                   src, ring_lds, (j + P - 1) % P, wave);
             nid0 = ids[min(2 * (pi + P), np - 1)];
             nid1 = ids[min(2 * (pi + P) + 1, np - 1)];
-            if constexpr (NRT > 0)
-                dma_step<D, F16, NRT, false, true>(j * SLOT, ((j + 1) % P) * SLOT, kPageSize, kPageSize, lb, qB, sc,
-                                                   vop, rm, Lsum, O, g, f, finv);
+            if constexpr (NRT > 0) {
+                // A causal item's pairs below every row's last token need no
+                // mask; the ones crossing the diagonal mask per row.
+                const int t = CAUSAL ? int(lim.tok0 + 2 * kPageSize * pi) : 0;
+                if (CAUSAL && t + 2 * kPageSize > int(lim.lmin))
+                    dma_step<D, F16, NRT, true, true>(j * SLOT, ((j + 1) % P) * SLOT,
+                                                      causal_mask<RT>(t, rtg.len, int(lim.lmax)), lb, qB, sc,
+                                                      vop, rm, Lsum, O, g, f, finv);
+                else
+                    dma_step<D, F16, NRT, false, true>(j * SLOT, ((j + 1) % P) * SLOT,
+                                                       uniform_mask<RT>(kPageSize, kPageSize), lb, qB, sc, vop,
+                                                       rm, Lsum, O, g, f, finv);
+            }
         });
     }
     // The last pair: its loads were waited for (vmcnt(0)) and made visible
@@ -1405,9 +1461,15 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
     // and reads no K, so it needs no barrier of its own.
     if constexpr (NRT > 0) {
         const uint32_t pl = nmain;
-        const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
-        const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
-        dma_step<D, F16, NRT, true, false>((pl % P) * SLOT, 0, n0, n1, lb, qB, sc, vop, rm, Lsum, O, g, f, finv);
+        PairMask<RT> pm;
+        if constexpr (CAUSAL) {
+            pm = causal_mask<RT>(int(lim.tok0 + 2 * kPageSize * pl), rtg.len, int(lim.lmax));
+        } else {
+            const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
+            const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
+            pm = uniform_mask<RT>(n0, n1);
+        }
+        dma_step<D, F16, NRT, true, false>((pl % P) * SLOT, 0, pm, lb, qB, sc, vop, rm, Lsum, O, g, f, finv);
     }
 }
 
@@ -1443,7 +1505,7 @@ __device__ __forceinline__ void write_partial_dma(const AttendArgs& a, const Ite
     }
 }
 
-template <int D, bool F16, int NRT>
+template <int D, bool F16, int NRT, bool PF>
 __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                               uint8_t* ring, int tid, int wave, int g, int c,
                                               const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
@@ -1461,10 +1523,17 @@ __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& i
         #pragma unroll
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    if (it.flags & kItemTail)
-        dma_group_loop<D, F16, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
-    else
-        dma_group_loop<D, F16, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
+    if constexpr (PF) {   // prefill plans: every item is causal
+        const ItemLim lim = a.item_lim[blockIdx.x];
+        dma_group_loop<D, F16, NRT, false, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm, L,
+                                                 O);
+    } else if (it.flags & kItemTail) {
+        dma_group_loop<D, F16, NRT, true, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+                                                 qB, rm, L, O);
+    } else {
+        dma_group_loop<D, F16, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+                                                  qB, rm, L, O);
+    }
     write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
 }
 
@@ -1483,7 +1552,7 @@ __device__ __forceinline__ Item uniform_item(const Item& it) {
     return u;
 }
 
-template <int D, bool F16>
+template <int D, bool F16, bool PF>
 __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& item, int tid, int wave, int g,
                                                int c) {
     using C = DmaCfg<D>;
@@ -1499,10 +1568,10 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
     // Tiles of this wave that hold rows: tiles w, w+4, ... below ceil(nrows/16).
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
-    if (nrt >= 3) dma_group_run<D, F16, C::RT>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else if (nrt == 2) dma_group_run<D, F16, 2>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else if (nrt == 1) dma_group_run<D, F16, 1>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else dma_group_run<D, F16, 0>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    if (nrt >= 3) dma_group_run<D, F16, C::RT, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 2) dma_group_run<D, F16, 2, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 1) dma_group_run<D, F16, 1, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else dma_group_run<D, F16, 0, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
 }
 
 // ------------------------------------------- group items, FP8 / MXFP8 KV
@@ -1672,10 +1741,11 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
     }
 }
 
-template <int D, uint32_t KVF, int NRT, bool TAIL>
+template <int D, uint32_t KVF, int NRT, bool TAIL, bool CAUSAL>
 __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                 uint8_t* ring, int tid, int wave, int g, int c,
                                                 const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
+                                                const ItemLim& lim,
                                                 u32x4 (&qB)[DmaCfg<D>::RT][D / 32],
                                                 RowMax<DmaCfg<D>::RT>& rm, f4 (&Lsum)[DmaCfg<D>::RT],
                                                 f4 (&O)[DmaCfg<D>::RT][D / 16]) {
@@ -1760,9 +1830,15 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
             if constexpr (NRT > 0) {
                 float ks0 = 1.f, ks1 = 1.f;
                 if constexpr (KS) k_scales(ps, ks0, ks1);
-                dma_step<D, false, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR, kPageSize,
-                                                         kPageSize, lb, qB, sc, vop, rm, Lsum, O, g, f, finv, ks0,
-                                                         ks1);
+                const int t = CAUSAL ? int(lim.tok0 + 2 * kPageSize * pi) : 0;
+                if (CAUSAL && t + 2 * kPageSize > int(lim.lmin))
+                    dma_step<D, false, NRT, true, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                                                            causal_mask<RT>(t, rtg.len, int(lim.lmax)), lb, qB, sc,
+                                                            vop, rm, Lsum, O, g, f, finv, ks0, ks1);
+                else
+                    dma_step<D, false, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                                                             uniform_mask<RT>(kPageSize, kPageSize), lb, qB, sc,
+                                                             vop, rm, Lsum, O, g, f, finv, ks0, ks1);
             }
             ps = psn;
             psn = psn + 1 == P ? 0 : psn + 1;
@@ -1772,16 +1848,22 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
     // the prologue); every raw load has landed (the last wait was vmcnt(0)).
     if constexpr (NRT > 0) {
         const uint32_t pl = nmain;
-        const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
-        const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
+        PairMask<RT> pm;
+        if constexpr (CAUSAL) {
+            pm = causal_mask<RT>(int(lim.tok0 + 2 * kPageSize * pl), rtg.len, int(lim.lmax));
+        } else {
+            const int n0 = TAIL && 2 * pl + 1 == np ? last_len : kPageSize;
+            const int n1 = 2 * pl + 1 >= np ? 0 : (TAIL && 2 * pl + 2 == np ? last_len : kPageSize);
+            pm = uniform_mask<RT>(n0, n1);
+        }
         float ks0 = 1.f, ks1 = 1.f;
         if constexpr (KS) k_scales(ps, ks0, ks1);
-        dma_step<D, false, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, n0, n1, lb, qB, sc, vop, rm, Lsum, O,
-                                                g, f, finv, ks0, ks1);
+        dma_step<D, false, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, pm, lb, qB, sc, vop, rm, Lsum, O, g,
+                                                f, finv, ks0, ks1);
     }
 }
 
-template <int D, uint32_t KVF, int NRT>
+template <int D, uint32_t KVF, int NRT, bool PF>
 __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                uint8_t* ring, int tid, int wave, int g, int c,
                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
@@ -1799,14 +1881,21 @@ __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& 
         #pragma unroll
         for (int e = 0; e < EPL; ++e) O[rt][e] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    if (it.flags & kItemTail)
-        dma8_group_loop<D, KVF, NRT, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
-    else
-        dma8_group_loop<D, KVF, NRT, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, qB, rm, L, O);
+    if constexpr (PF) {   // prefill plans: every item is causal
+        const ItemLim lim = a.item_lim[blockIdx.x];
+        dma8_group_loop<D, KVF, NRT, false, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm,
+                                                  L, O);
+    } else if (it.flags & kItemTail) {
+        dma8_group_loop<D, KVF, NRT, true, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+                                                  qB, rm, L, O);
+    } else {
+        dma8_group_loop<D, KVF, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+                                                   qB, rm, L, O);
+    }
     write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
 }
 
-template <int D, uint32_t KVF>
+template <int D, uint32_t KVF, bool PF>
 __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item& item, int tid, int wave, int g,
                                                 int c) {
     using C = DmaCfg<D>;
@@ -1821,9 +1910,9 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
     __syncthreads();
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
-    if (nrt >= 2) dma8_group_run<D, KVF, C::RT>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else if (nrt == 1) dma8_group_run<D, KVF, 1>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else dma8_group_run<D, KVF, 0>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    if (nrt >= 2) dma8_group_run<D, KVF, C::RT, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 1) dma8_group_run<D, KVF, 1, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else dma8_group_run<D, KVF, 0, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
 }
 
 // ---------------------------------------------------------------- attend16
@@ -1837,12 +1926,26 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     if (blockIdx.x < a.n_group_items) {
         const Item it = a.items[blockIdx.x];
         if constexpr ((KVF == KVF_FP8 || KVF == KVF_MX) && D == 64) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
-        else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF>(a, it, tid, wave, g, c);
-        else group_item_dma<D, F16>(a, it, tid, wave, g, c);
+        else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, false>(a, it, tid, wave, g, c);
+        else group_item_dma<D, F16, false>(a, it, tid, wave, g, c);
     } else {
         const uint32_t idx = wave_item_index(a, wave);
         if (idx < a.n_group_items + a.n_wave_items) wave_item<D, KVF, F16>(a, a.items[idx], g, c);
     }
+}
+
+// Prefill plans: causal group items only (every workgroup one item); the
+// 16-bit and FP8 / MXFP8 direct-load paths at head_dim 128 and 256 and the
+// 16-bit one at 64.  A kernel of its own, so the per-row token masks do not
+// add to the decode kernel's registers.
+template <int D, uint32_t KVF, bool F16>
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill16_kernel(AttendArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (blockIdx.x >= a.n_group_items) return;
+    const Item it = a.items[blockIdx.x];
+    if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, true>(a, it, tid, wave, g, c);
+    else group_item_dma<D, F16, true>(a, it, tid, wave, g, c);
 }
 
 // ---------------------------------------------------------------- attend32
@@ -2095,6 +2198,23 @@ __global__ __launch_bounds__(256) void scatter_kernel(uint8_t* dst, const uint8_
 }
 
 template <int D>
+hipError_t launch_prefill_d(const AttendArgs& a, uint32_t n, uint32_t q_dtype, uint32_t kvf, hipStream_t s) {
+    dim3 grid(n), block(kWaves * 64);
+    if (q_dtype == 1 && kvf == KVF_BF16) {
+        hipLaunchKernelGGL((prefill16_kernel<D, KVF_BF16, false>), grid, block, 0, s, a);
+    } else if (q_dtype == 0 && kvf == KVF_F16) {
+        hipLaunchKernelGGL((prefill16_kernel<D, KVF_F16, true>), grid, block, 0, s, a);
+    } else if constexpr (D >= 128) {
+        if (q_dtype == 1 && kvf == KVF_FP8) hipLaunchKernelGGL((prefill16_kernel<D, KVF_FP8, false>), grid, block, 0, s, a);
+        else if (q_dtype == 1 && kvf == KVF_MX) hipLaunchKernelGGL((prefill16_kernel<D, KVF_MX, false>), grid, block, 0, s, a);
+        else return hipErrorInvalidValue;
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int D>
 hipError_t launch_attend_d(const AttendArgs& a, uint32_t n, uint32_t q_dtype, uint32_t kvf,
                            hipStream_t s) {
     dim3 grid(n), block(kWaves * 64);
@@ -2135,9 +2255,17 @@ bool attend_supported(uint32_t q_dtype, uint32_t kvf, uint32_t d) {
 }
 
 int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint32_t kvf,
-                  uint32_t d, void* stream) {
+                  uint32_t d, bool prefill, void* stream) {
     if (n_items == 0) return hipSuccess;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (prefill) {
+        switch (d) {
+            case 64: return launch_prefill_d<64>(a, n_items, q_dtype, kvf, s);
+            case 128: return launch_prefill_d<128>(a, n_items, q_dtype, kvf, s);
+            case 256: return launch_prefill_d<256>(a, n_items, q_dtype, kvf, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (d) {
         case 64: return launch_attend_d<64>(a, n_items, q_dtype, kvf, s);
         case 128: return launch_attend_d<128>(a, n_items, q_dtype, kvf, s);

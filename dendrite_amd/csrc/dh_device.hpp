@@ -50,6 +50,16 @@ struct Item {
     uint32_t tail_seq;
 };
 constexpr uint32_t kItemTail = 1u;
+// kItemCausal (prefill): the item's rows see different numbers of tokens,
+// row_len[row's virtual sequence] each; ItemLim bounds them.
+constexpr uint32_t kItemCausal = 2u;
+
+// Token range of a causal item: its pages start at token tok0 of the
+// sequence; its rows see lmin .. lmax tokens (lmin > tok0, lmax <= the
+// tokens its pages hold).
+struct ItemLim {
+    uint32_t tok0, lmin, lmax, pad;
+};
 
 // What one workgroup does: up to four wave items (one per wave, <= 16 rows
 // each) or one group item (<= group_rows() rows: each wave owns a block of
@@ -96,6 +106,10 @@ struct AttendArgs {
                                  // kernels see scale_log2 > 0 and may order scaled
                                  // scores by raw ones
     uint32_t n_group_items, n_wave_items;
+    // Prefill plans (kItemCausal items): tokens each virtual sequence sees,
+    // and the group items' token ranges; null for decode plans.
+    const uint32_t* row_len;
+    const ItemLim* item_lim;
 };
 
 struct MergeArgs {
@@ -124,7 +138,7 @@ int launch_write_pages(const uint32_t* ids, uint32_t n, const void* src, uint32_
                        uint8_t* scales, uint32_t num_pages, uint32_t hkv, uint32_t d, uint32_t fmt,
                        void* stream);
 int launch_attend(const AttendArgs& a, uint32_t n_tasks, uint32_t q_dtype, uint32_t kv_format,
-                  uint32_t head_dim, void* stream);
+                  uint32_t head_dim, bool prefill, void* stream);
 int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t head_dim, void* stream);
 int launch_merge_states(const float* o_a, const float* lse_a, const float* o_b,
                         const float* lse_b, float* o_out, float* lse_out, uint32_t n_rows,

@@ -436,4 +436,156 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     return DH_OK;
 }
 
+// Prefill items: for each sequence, KV head and block of query tokens
+// (group_rows / r tokens, their r heads each a row), the KV pages the block's
+// last query sees, cut into chunks of chunk_pages.  Chunk starts stay below
+// the block's first query's token count (the last chunk absorbs the rest,
+// the diagonal included), so every row sees at least one token of every
+// item it is in.  Items: heaviest first; one workgroup each.
+int build_prefill_plan(const PrefillInput& in, HostPlan& out, std::string& err) {
+    out = HostPlan();
+    const uint32_t B = in.batch;
+    if (in.hkv == 0 || in.hq % in.hkv != 0) {
+        err = "num_heads must be divisible by num_kv_heads";
+        return DH_EINVAL;
+    }
+    const uint32_t r = in.hq / in.hkv;
+    if (r > in.group_rows) {
+        err = "more query heads per KV head than rows in a work item";
+        return DH_EUNSUPPORTED;
+    }
+    const uint32_t tpb = in.group_rows / r;   // query tokens per block
+    // Page lists (INVALID dropped) and the virtual sequences.
+    std::vector<std::vector<uint32_t>> pl(B);
+    std::vector<uint32_t> q_off(B + 1, 0);
+    for (uint32_t b = 0; b < B; ++b) {
+        if (in.indptr[b + 1] < in.indptr[b]) {
+            err = "indptr must be non-decreasing";
+            return DH_EINVAL;
+        }
+        for (uint32_t k = in.indptr[b]; k < in.indptr[b + 1]; ++k) {
+            const uint32_t p = in.indices[k];
+            if (p == DH_INVALID_PAGE) continue;
+            if (p >= in.num_pool_pages) {
+                err = "page id " + std::to_string(p) + " outside the pool (sequence " + std::to_string(b) + ")";
+                return DH_EINVAL;
+            }
+            pl[b].push_back(p);
+        }
+        const uint64_t np = pl[b].size(), kv = in.kv_len[b], q = in.q_len[b];
+        if (kv > np * kPageSize || (np && kv <= (np - 1) * kPageSize) || (!np && kv)) {
+            err = "sequence " + std::to_string(b) + ": " + std::to_string(kv) + " tokens do not fill its " +
+                  std::to_string(np) + " pages (the last one holds 1..16)";
+            return DH_EINVAL;
+        }
+        if (q > kv) {
+            err = "sequence " + std::to_string(b) + ": more queries than tokens";
+            return DH_EINVAL;
+        }
+        if (kv > DH_MAX_SEQ_LEN) {
+            err = "sequence " + std::to_string(b) + " exceeds MAX_SEQ_LEN";
+            return DH_EINVAL;
+        }
+        q_off[b + 1] = q_off[b] + uint32_t(q);
+        out.total_pages += np;
+    }
+    const uint32_t nq = q_off[B];
+    out.row_len.resize(nq);
+    for (uint32_t b = 0; b < B; ++b)
+        for (uint32_t i = 0; i < in.q_len[b]; ++i)
+            out.row_len[q_off[b] + i] = in.causal ? in.kv_len[b] - in.q_len[b] + i + 1 : in.kv_len[b];
+    auto len_of = [&](uint32_t b, uint32_t i) { return out.row_len[q_off[b] + i]; };
+
+    // Chunk size: one chunk per block when blocks alone fill the chip.
+    uint64_t n_blocks = 0;
+    for (uint32_t b = 0; b < B; ++b) n_blocks += (in.q_len[b] + tpb - 1) / tpb;
+    uint32_t chunk = in.chunk_pages;
+    if (!chunk) chunk = n_blocks * in.hkv >= 512 ? UINT32_MAX : 32;
+
+    // Blocks and their chunks: (sequence, token range, page range).
+    struct Piece {
+        uint32_t b, i0, i1, p0, p1;
+    };
+    std::vector<Piece> pieces;
+    for (uint32_t b = 0; b < B; ++b) {
+        for (uint32_t i0 = 0; i0 < in.q_len[b]; i0 += tpb) {
+            const uint32_t i1 = std::min(in.q_len[b], i0 + tpb);
+            const uint32_t lmin = len_of(b, i0), lmax = len_of(b, i1 - 1);
+            const uint32_t pend = (lmax + kPageSize - 1) / kPageSize;
+            const uint32_t plast = (lmin - 1) / kPageSize;       // a chunk may start at or below this page
+            uint32_t p0 = 0;
+            while (true) {
+                const uint64_t nx = uint64_t(p0) + chunk;
+                if (nx > plast || nx >= pend) {
+                    pieces.push_back(Piece{b, i0, i1, p0, pend});
+                    break;
+                }
+                pieces.push_back(Piece{b, i0, i1, p0, uint32_t(nx)});
+                p0 = uint32_t(nx);
+            }
+        }
+    }
+    // Partial slots: one per (chunk, query), contiguous per query.
+    std::vector<uint32_t> count(nq, 0);
+    for (const Piece& pc : pieces)
+        for (uint32_t i = pc.i0; i < pc.i1; ++i) count[q_off[pc.b] + i]++;
+    out.slot_ptr.assign(nq + 1, 0);
+    for (uint32_t v = 0; v < nq; ++v) out.slot_ptr[v + 1] = out.slot_ptr[v] + count[v];
+    out.num_slots = out.slot_ptr[nq];
+    std::vector<uint32_t> cursor(out.slot_ptr.begin(), out.slot_ptr.end() - 1);
+    // Page lists into the plan, one copy per sequence.
+    std::vector<uint32_t> page_base(B);
+    for (uint32_t b = 0; b < B; ++b) {
+        page_base[b] = uint32_t(out.pages.size());
+        out.pages.insert(out.pages.end(), pl[b].begin(), pl[b].end());
+    }
+    struct Cand {
+        double cost;
+        Item it;
+        ItemLim lim;
+    };
+    std::vector<Cand> cands;
+    for (const Piece& pc : pieces) {
+        const uint32_t seq_off = uint32_t(out.seqslots.size());
+        for (uint32_t i = pc.i0; i < pc.i1; ++i) {
+            const uint32_t v = q_off[pc.b] + i;
+            out.seqslots.push_back(SeqSlot{v, cursor[v]++});
+        }
+        const uint32_t tok0 = pc.p0 * kPageSize, tok_end = std::min(pc.p1 * kPageSize, in.kv_len[pc.b]);
+        ItemLim lim;
+        lim.tok0 = tok0;
+        lim.lmin = std::min(len_of(pc.b, pc.i0), tok_end);
+        lim.lmax = std::min(len_of(pc.b, pc.i1 - 1), tok_end);
+        lim.pad = 0;
+        for (uint32_t h = 0; h < in.hkv; ++h) {
+            Item it;
+            it.page_off = page_base[pc.b] + pc.p0;
+            it.npages = pc.p1 - pc.p0;
+            it.seq_off = seq_off;
+            it.row_begin = 0;
+            it.nrows = (pc.i1 - pc.i0) * r;
+            it.kv_head = h;
+            it.flags = kItemCausal;
+            it.tail_seq = 0;
+            const double cost = double(it.npages) * (2.0 + (it.nrows + kTileRows - 1) / kTileRows);
+            cands.push_back(Cand{cost, it, lim});
+        }
+        out.page_reads += uint64_t(pc.p1 - pc.p0);
+    }
+    std::stable_sort(cands.begin(), cands.end(), [](const Cand& x, const Cand& y) { return x.cost > y.cost; });
+    for (const Cand& c : cands) {
+        out.tasks.push_back(Task{kTaskGroup, uint32_t(out.items.size()), 1u, 0u});
+        out.items.push_back(c.it);
+        out.item_lim.push_back(c.lim);
+    }
+    out.num_group_items = uint32_t(out.items.size());
+    out.num_wave_items = 0;
+    out.num_segments = uint32_t(pieces.size());
+    out.num_shared_segments = 0;
+    uint64_t uniq = 0;
+    for (uint32_t b = 0; b < B; ++b) uniq += pl[b].size();
+    out.unique_pages = uniq;
+    return DH_OK;
+}
+
 }  // namespace dh

@@ -35,9 +35,31 @@ struct HostPlan {
     uint64_t unique_pages = 0;
     uint64_t page_reads = 0;            // pages read per KV head per step
     uint64_t total_pages = 0;
+    // Prefill plans: tokens each virtual sequence (query) sees, and each
+    // (causal) item's token range.
+    std::vector<uint32_t> row_len;
+    std::vector<ItemLim> item_lim;
+};
+
+// Prefill: sequence b holds kv_len[b] tokens in its pages (CSR as for
+// decode); its last q_len[b] tokens are queries, each a virtual sequence
+// (rows of q / out in order).  Causal: query i sees kv_len - q_len + i + 1
+// tokens, else all kv_len.
+struct PrefillInput {
+    uint32_t batch = 0;
+    const uint32_t* indptr = nullptr;
+    const uint32_t* indices = nullptr;
+    const uint32_t* kv_len = nullptr;
+    const uint32_t* q_len = nullptr;
+    uint32_t num_pool_pages = 0;
+    uint32_t hq = 0, hkv = 0;
+    uint32_t group_rows = 128;
+    bool causal = true;
+    uint32_t chunk_pages = 0;           // 0 = chosen from the work
 };
 
 // Returns 0 on success, else a dh_status code with `err` set.
 int build_plan(const PlanInput& in, HostPlan& out, std::string& err);
+int build_prefill_plan(const PrefillInput& in, HostPlan& out, std::string& err);
 
 }  // namespace dh

@@ -281,6 +281,26 @@ dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages,
                           uint32_t* pages, uint32_t* n_pages,
                           uint32_t* seqslots, uint32_t* n_seqslots);
 
+/* Prefill plan (paged, causal).  Sequence b holds kv_len[b] tokens in its
+ * pages (indptr / indices as for dh_plan_create, INVALID skipped; the last
+ * page holds 1..16 of them) of which the last q_len[b] are the queries: rows
+ * q_off[b] .. q_off[b] + q_len[b] of q and out (q_off = prefix sums of
+ * q_len), each [num_heads][head_dim].  With causal != 0 query i of sequence
+ * b sees tokens 0 .. kv_len[b] - q_len[b] + i (the bottom-right-aligned mask
+ * of FA2 / FlashInfer); else all kv_len[b].  Run with dh_decode_batch (q /
+ * out [sum q_len][num_heads][head_dim], last_page_len ignored).  Covers
+ * ReferenceBackend::prefill (attention/backend.rs:163-204: q_len = kv_len,
+ * causal) and BatchPrefillKernel::run (flashinfer/batch_prefill.rs:86-101,
+ * K/V written to pages first); chunked prefill over a cached context is
+ * q_len < kv_len.  bf16 / f16 queries; FP8 / MXFP8 KV at head_dim 128 and
+ * 256.  chunk_pages: KV pages per work item (0 = chosen from the work).
+ * Host-side, synchronous. */
+dh_status dh_plan_create_prefill(dh_backend* backend, const dh_attn_config* cfg,
+                                 const dh_pool* pool, const uint32_t* indptr,
+                                 const uint32_t* indices, const uint32_t* kv_len,
+                                 const uint32_t* q_len, uint32_t batch_size, uint32_t causal,
+                                 uint32_t chunk_pages, dh_plan** out);
+
 /* ------------------------------------------------------------------ decode */
 
 /* One decode step: out[b][h][:] = softmax(q[b][h] . K_b^T * scale) . V_b for
