@@ -130,11 +130,20 @@ def test_backend_tree_decode_matches_oracle(kvf):
     assert np.max(np.abs(got - want)) < tol
 
 
-def test_prefill_is_unsupported():
+def test_prefill_errors():
+    """prefill takes bf16 / f16 queries (f32: DH_EUNSUPPORTED) and key /
+    value of the query's batch and length (else DH_EINVAL)."""
+    import torch
     be = HipBackend(num_pages=4, num_kv_heads=4, head_dim=64)
+    cfg = AttentionConfig(4, 4, 64)
+    q = torch.zeros(1, 4, 8, 64)
     with pytest.raises(DhError) as e:
-        be.prefill(None, None, None, BlockTable(16), AttentionConfig(4, 4, 64))
+        be.prefill(q, q, q, BlockTable(16), cfg)
     assert e.value.status == _lib.DH_EUNSUPPORTED
+    qb = q.to(torch.bfloat16)
+    with pytest.raises(DhError) as e:
+        be.prefill(qb, qb[:, :, :5], qb[:, :, :5], BlockTable(16), cfg)
+    assert e.value.status == _lib.DH_EINVAL
 
 
 @pytest.mark.parametrize("kvf", [_lib.KV_BF16, _lib.KV_FP8_E4M3, _lib.KV_MXFP8])
