@@ -29,6 +29,7 @@ KV_F16, KV_BF16, KV_F32, KV_FP8_E4M3, KV_MXFP8 = 0, 1, 2, 3, 4
 GQA_TILED, GQA_INTERLEAVED = 0, 1
 # plan flags
 PLAN_FLAT, PLAN_CASCADE = 0, 1
+PLAN_APPEND, PLAN_REPLACE_LAST = 0, 1
 
 PAGE_SIZE = 16
 MAX_SEQ_LEN = 131072
@@ -111,6 +112,7 @@ SIGNATURES = {
     "dh_plan_create_prefill": (_I, [_P, C.POINTER(dh_attn_config), _P, _PU32, _PU32, _PU32, _PU32, _U32, _U32,
                                     _U32, C.POINTER(_P)]),
     "dh_plan_destroy": (_I, [_P]),
+    "dh_plan_update": (_I, [_P, _U32, _PU32, _PU32, _PU32, _P, _PU32]),
     "dh_plan_workspace_size": (C.c_size_t, [_P]),
     "dh_plan_get_stats": (_I, [_P, C.POINTER(dh_plan_stats)]),
     "dh_plan_inspect": (_I, [_P, _U32, _PU32, _PU32, _U32, _U32, _P, C.POINTER(dh_plan_stats), _P, _PU32,

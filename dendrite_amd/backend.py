@@ -265,6 +265,18 @@ class DecodePlan:
             destroy(self._h)
             self._h = None
 
+    def update(self, events, stream=None) -> bool:
+        """dh_plan_update: apply [(sequence, op, page_id)] (op PLAN_APPEND or
+        PLAN_REPLACE_LAST) in place on the stream; False when they do not fit
+        and a new plan is needed (nothing changed then)."""
+        ev = np.asarray(list(events), dtype=np.uint32).reshape(-1, 3)
+        seqs, ops, ids = (np.ascontiguousarray(ev[:, i]) for i in range(3))
+        patched = C.c_uint32()
+        check(lib().dh_plan_update(self._h, len(ev), seqs.ctypes.data_as(_lib._PU32),
+                                   ops.ctypes.data_as(_lib._PU32), ids.ctypes.data_as(_lib._PU32),
+                                   C.c_void_p(_stream_ptr(stream)), C.byref(patched)))
+        return bool(patched.value)
+
     def stats(self) -> dict:
         s = _lib.dh_plan_stats()
         check(lib().dh_plan_get_stats(self._h, C.byref(s)))
@@ -342,6 +354,81 @@ def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream
                                  lpl, C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()),
                                  workspace.numel() * workspace.element_size(), stages,
                                  C.c_void_p(_stream_ptr(stream))))
+
+
+class TreeDecoder:
+    """Decode steps over the leaves of a TreeState (tree/state.rs) with one
+    cascade plan kept current from the tree's own events.
+
+    append_token(i, token) runs TreeState::append_token on leaf i
+    (tree/state.rs:87-113) and records what it did to the leaf's page list:
+    a block allocated on a block boundary (PLAN_APPEND), or the copy-on-write
+    of a shared partial last block, whose page data it copies
+    (dh_pool_copy_page) before recording PLAN_REPLACE_LAST.  It returns
+    (page, offset) where the new token's K / V go; writing them is the
+    caller's (append_kv).  fork(i) adds a leaf (TreeState::fork, :49-84).
+    decode(q) applies the recorded events to the plan in place
+    (dh_plan_update) and builds a new plan from the tree's block tables only
+    when they do not fit or the set of leaves changed.  Leaves are the plan's
+    sequences, in order; q / out are device tensors [leaves][Hq][D]."""
+
+    def __init__(self, backend: Backend, pool: Pool, tree, config: AttentionConfig, leaves):
+        self.backend = backend
+        self.pool = pool
+        self.tree = tree
+        self.config = config
+        self.leaves = [int(n) for n in leaves]
+        self._plan: Optional[DecodePlan] = None
+        self._ws = None
+        self._events: list[tuple[int, int, int]] = []
+        self.plans_built = 0
+        self.plans_patched = 0
+
+    def fork(self, i: int) -> int:
+        """Forks leaf i into a new leaf (appended last); returns its index."""
+        self.leaves.append(int(self.tree.fork(self.leaves[i]).node_id))
+        self._plan = None
+        return len(self.leaves) - 1
+
+    def append_token(self, i: int, token: int, stream=None) -> tuple[int, int]:
+        node = self.leaves[i]
+        n = self.tree.get_node(node).num_tokens
+        cow = self.tree.append_token(node, token)
+        if cow is not None:
+            self.pool.copy_page(int(cow[0]), int(cow[1]), stream)
+            self._events.append((i, _lib.PLAN_REPLACE_LAST, int(cow[1])))
+        table = self.tree.get_block_table(node)
+        if n % _lib.PAGE_SIZE == 0:
+            self._events.append((i, _lib.PLAN_APPEND, int(table[-1])))
+        return int(table[n // _lib.PAGE_SIZE]), n % _lib.PAGE_SIZE
+
+    def tables(self) -> list[list[int]]:
+        return [[int(b) for b in self.tree.get_block_table(n)] for n in self.leaves]
+
+    def last_page_len(self) -> np.ndarray:
+        return np.array([self.tree.get_node(n).num_tokens % _lib.PAGE_SIZE for n in self.leaves], np.int32)
+
+    def decode(self, q, out=None, stream=None):
+        torch = _torch()
+        if self._plan is not None and self._events:
+            if self._plan.update(self._events, stream):
+                self.plans_patched += 1
+            else:
+                self._plan = None
+        self._events = []
+        if self._plan is None:
+            tables = self.tables()
+            indptr = np.cumsum([0] + [len(t) for t in tables]).astype(np.uint32)
+            indices = np.array([b for t in tables for b in t], dtype=np.uint32)
+            self._plan = DecodePlan(self.backend, self.config, self.pool, indptr, indices)
+            self._ws = self._plan.workspace()
+            self.plans_built += 1
+        dev = f"cuda:{self.backend.device}"
+        lpl = torch.from_numpy(self.last_page_len()).to(dev)   # 0 reads as a full page
+        if out is None:
+            out = torch.empty_like(q)
+        decode_batch(self._plan, q, out, self._ws, lpl, stream)
+        return out
 
 
 class HipBackend:

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <math.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -132,6 +133,10 @@ struct dh_plan {
     dh_plan_stats stats;
     size_t ws_bytes;
     size_t ws_lse_off;
+    // Decode plans: host copies of the last-chunk tables (HostPlan::tail_*)
+    // for dh_plan_update, and where items and pages start in dev (words).
+    std::vector<uint32_t> tail_off, tail_n, tail_cap, tail_item_ptr, tail_items;
+    size_t items_word, pages_word;
 };
 
 extern "C" {
@@ -534,9 +539,8 @@ dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages, co
 // per-query token counts and item token ranges) in one device blob.
 static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
                              const dh::HostPlan& hp, uint32_t batch, bool prefill, dh_plan** out) {
-    dh_plan* pl = new (std::nothrow) dh_plan;
+    dh_plan* pl = new (std::nothrow) dh_plan();
     if (!pl) return fail(DH_ENOMEM, "out of host memory");
-    memset(pl, 0, sizeof *pl);
     pl->be = be;
     pl->cfg = *cfg;
     pl->batch = batch;
@@ -584,6 +588,15 @@ static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh
     pl->ws_lse_off = align_up(rows * cfg->head_dim * o_bytes, 256);
     pl->ws_bytes = align_up(pl->ws_lse_off + rows * sizeof(dh::PartialLse), 256);
     fill_stats(hp, batch, &pl->stats);
+    if (!prefill) {
+        pl->tail_off = hp.tail_off;
+        pl->tail_n = hp.tail_n;
+        pl->tail_cap = hp.tail_cap;
+        pl->tail_item_ptr = hp.tail_item_ptr;
+        pl->tail_items = hp.tail_items;
+    }
+    pl->items_word = o_items / sizeof(uint32_t);
+    pl->pages_word = o_pages / sizeof(uint32_t);
     retain(be);
     *out = pl;
     return DH_OK;
@@ -643,6 +656,79 @@ dh_status dh_plan_create_prefill(dh_backend* be, const dh_attn_config* cfg, cons
     const int rc = dh::build_prefill_plan(in, hp, err);
     if (rc != DH_OK) return fail(dh_status(rc), "%s", err.c_str());
     return upload_plan(be, cfg, pool, hp, uint32_t(hp.row_len.size()), true, out);
+}
+
+dh_status dh_plan_update(dh_plan* pl, uint32_t n, const uint32_t* seqs, const uint32_t* ops,
+                         const uint32_t* page_ids, void* stream, uint32_t* patched) {
+    static_assert(sizeof(dh::Item) == 8 * sizeof(uint32_t) && offsetof(dh::Item, npages) == sizeof(uint32_t),
+                  "Item.npages is word 1 of 8");
+    if (!pl || !patched) return fail(DH_EINVAL, "NULL argument");
+    *patched = 0;
+    if (pl->prefill) return fail(DH_EUNSUPPORTED, "prefill plans are not updated in place");
+    if (n && (!seqs || !ops || !page_ids)) return fail(DH_EINVAL, "NULL argument");
+    // Validate every event and check that all fit before changing anything.
+    std::vector<std::pair<uint32_t, uint32_t>> count;   // (sequence, pages in its last chunk)
+    auto find = [&](uint32_t b) -> uint32_t& {
+        for (auto& c : count)
+            if (c.first == b) return c.second;
+        count.emplace_back(b, pl->tail_n[b]);
+        return count.back().second;
+    };
+    bool fits = true;
+    uint32_t appended = 0;
+    for (uint32_t k = 0; k < n; ++k) {
+        if (seqs[k] >= pl->batch)
+            return fail(DH_EINVAL, "event %u: sequence %u outside the plan's batch of %u", k, seqs[k], pl->batch);
+        if (ops[k] != DH_PLAN_APPEND && ops[k] != DH_PLAN_REPLACE_LAST)
+            return fail(DH_EINVAL, "event %u: unknown op %u", k, ops[k]);
+        if (page_ids[k] >= pl->pool_pages)
+            return fail(DH_EINVAL, "event %u: page id %u outside the pool of %u pages", k, page_ids[k],
+                        pl->pool_pages);
+        uint32_t& c = find(seqs[k]);
+        if (c == 0) fits = false;                       // no pages: no chunk to patch
+        else if (ops[k] == DH_PLAN_APPEND) {
+            if (c == pl->tail_cap[seqs[k]]) fits = false;
+            else ++c, ++appended;
+        }
+    }
+    if (!fits) return DH_OK;
+    // The words to write: page ids in event order, then each changed chunk's
+    // page count in every item of it.
+    std::vector<uint32_t> idx, val;
+    for (auto& c : count) c.second = pl->tail_n[c.first];
+    for (uint32_t k = 0; k < n; ++k) {
+        const uint32_t b = seqs[k];
+        uint32_t& c = find(b);
+        if (ops[k] == DH_PLAN_APPEND) ++c;
+        idx.push_back(uint32_t(pl->pages_word + pl->tail_off[b] + c - 1));
+        val.push_back(page_ids[k]);
+    }
+    for (const auto& c : count) {
+        if (c.second == pl->tail_n[c.first]) continue;
+        for (uint32_t t = pl->tail_item_ptr[c.first]; t < pl->tail_item_ptr[c.first + 1]; ++t) {
+            idx.push_back(uint32_t(pl->items_word + size_t(pl->tail_items[t]) * 8 + 1));
+            val.push_back(c.second);
+        }
+    }
+    {
+        dh::DeviceGuard guard(pl->be->device);
+        hipError_t e = guard.error();
+        for (size_t o = 0; e == hipSuccess && o < idx.size(); o += dh::kPatchWords) {
+            const uint32_t m = uint32_t(std::min<size_t>(dh::kPatchWords, idx.size() - o));
+            e = hipError_t(dh::launch_plan_patch(reinterpret_cast<uint32_t*>(pl->dev), m, idx.data() + o,
+                                                 val.data() + o, stream));
+        }
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(DH_EHIP, "plan update failed: %s", hipGetErrorString(e));
+        }
+    }
+    for (const auto& c : count) pl->tail_n[c.first] = c.second;
+    pl->stats.total_pages += appended;
+    pl->stats.page_reads += appended;
+    pl->stats.unique_pages += appended;   // a new block is read by its sequence alone
+    *patched = 1;
+    return DH_OK;
 }
 
 dh_status dh_plan_destroy(dh_plan* pl) {

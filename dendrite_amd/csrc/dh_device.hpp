@@ -134,6 +134,10 @@ DH_HOST_DEVICE inline uint64_t plane_offset(uint32_t page, uint32_t plane, uint3
 // Return hipError_t as int.
 extern "C++" {
 namespace dh {
+// Plan patches: words[idx[k]] = val[k] for k < n, in order, one small
+// kernel on the stream (n <= kPatchWords).
+constexpr uint32_t kPatchWords = 128;
+int launch_plan_patch(uint32_t* words, uint32_t n, const uint32_t* idx, const uint32_t* val, void* stream);
 int launch_write_pages(const uint32_t* ids, uint32_t n, const void* src, uint32_t src_dtype, uint8_t* data,
                        uint8_t* scales, uint32_t num_pages, uint32_t hkv, uint32_t d, uint32_t fmt,
                        void* stream);

@@ -321,6 +321,9 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
 
     // 5. Items.  Group items that read the same pages are kept together.
     std::vector<Group> groups;      // group items by (segment, chunk, head)
+    out.tail_off.assign(B, 0);
+    out.tail_n.assign(B, 0);
+    out.tail_cap.assign(B, 0);
     std::vector<std::pair<double, Item>> waves;
     // Distinct pages of the plan, for the statistics: a bitmap over the pool.
     std::vector<uint64_t> seen((uint64_t(in.num_pool_pages) + 63) / 64, 0);
@@ -331,6 +334,15 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         const uint32_t np = uint32_t(sg.pages.size());
         const uint32_t base = uint32_t(out.pages.size());
         out.pages.insert(out.pages.end(), sg.pages.begin(), sg.pages.end());
+        if (sg.tail) {
+            // Room for the sequence's last chunk to grow in place.
+            const uint32_t b = sg.seqs[0];
+            const uint32_t p0 = uint32_t(uint64_t(nchunks[s] - 1) * sg.pages.size() / nchunks[s]);
+            out.tail_off[b] = base + p0;
+            out.tail_n[b] = uint32_t(sg.pages.size()) - p0;
+            out.tail_cap[b] = std::max(out.tail_n[b], std::min<uint32_t>(out.tail_n[b] + kTailSlack, kMaxItemPages));
+            out.pages.insert(out.pages.end(), out.tail_cap[b] - out.tail_n[b], DH_INVALID_PAGE);
+        }
         for (uint32_t p : sg.pages) {
             const uint64_t bit = 1ull << (p & 63);
             uniq += (seen[p >> 6] & bit) == 0;
@@ -419,6 +431,17 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     }
     out.num_group_items = uint32_t(gorder.size());
     out.num_wave_items = uint32_t(waves.size());
+    // The items of each sequence's last chunk, by final item index.
+    out.tail_item_ptr.assign(B + 1, 0);
+    for (const Item& it : out.items)
+        if (it.flags & kItemTail) out.tail_item_ptr[it.tail_seq + 1]++;
+    for (uint32_t b = 0; b < B; ++b) out.tail_item_ptr[b + 1] += out.tail_item_ptr[b];
+    out.tail_items.resize(out.tail_item_ptr[B]);
+    {
+        std::vector<uint32_t> fill(out.tail_item_ptr.begin(), out.tail_item_ptr.end() - 1);
+        for (uint32_t i = 0; i < uint32_t(out.items.size()); ++i)
+            if (out.items[i].flags & kItemTail) out.tail_items[fill[out.items[i].tail_seq]++] = i;
+    }
     // The attention kernel derives a workgroup's items from its index alone
     // (AttendArgs): group task b runs item b, wave task b runs items
     // G + 4 (b - G) + w.  Check the emitted tasks against that mapping.

@@ -7,6 +7,13 @@
 
 namespace dh {
 
+// Pages reserved after each sequence's last chunk, so a decode plan can take
+// that many appended pages in place; no item holds more than kMaxItemPages
+// (a wave item keeps its page ids in registers, four per lane; a group item
+// in a 256-entry LDS list).
+constexpr uint32_t kTailSlack = 16;
+constexpr uint32_t kMaxItemPages = 256;
+
 struct PlanInput {
     uint32_t batch = 0;
     const uint32_t* indptr = nullptr;   // [batch + 1]
@@ -39,6 +46,13 @@ struct HostPlan {
     // (causal) item's token range.
     std::vector<uint32_t> row_len;
     std::vector<ItemLim> item_lim;
+    // Decode plans, per sequence b: the chunk holding its last page, for
+    // in-place updates (appending a page, replacing the last page).  Its
+    // pages are pages[tail_off[b] .. + tail_n[b]) and the entries up to
+    // tail_cap[b] are reserved (DH_INVALID_PAGE); its items (one per KV head
+    // and row block) are tail_items[tail_item_ptr[b] .. tail_item_ptr[b + 1]).
+    // tail_n[b] = 0: the sequence has no pages.
+    std::vector<uint32_t> tail_off, tail_n, tail_cap, tail_item_ptr, tail_items;
 };
 
 // Prefill: sequence b holds kv_len[b] tokens in its pages (CSR as for

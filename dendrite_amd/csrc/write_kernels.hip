@@ -2,6 +2,9 @@
 // ReferenceBackend::append_kv / store_kv (crates/dendrite-core/src/attention/
 // backend.rs:285-301, 140-143) for K/V already resident in HBM.
 //
+// Also the plan patch kernel (dh_plan_update): a few words of a decode
+// plan's device tables rewritten in stream order.
+//
 // A source page is [2][num_kv_heads][16][head_dim] elements (K plane, then
 // V; tokens past a partial page's length are zero) of f32, bf16 or f16.  It
 // becomes page page_ids[i] of the pool in the pool's format:
@@ -211,7 +214,35 @@ hipError_t launch_write_src(const WriteArgs& w, uint32_t src_dtype, uint32_t fmt
     }
 }
 
+struct PatchArgs {
+    uint32_t* words;
+    uint32_t n;
+    uint32_t idx[kPatchWords];
+    uint32_t val[kPatchWords];
+};
+
+// One lane applies the patches in order (a later write to the same word
+// wins); a handful of words per decode step.
+__global__ __launch_bounds__(64) void plan_patch_kernel(PatchArgs a) {
+    if (threadIdx.x != 0) return;
+    for (uint32_t k = 0; k < a.n; ++k) a.words[a.idx[k]] = a.val[k];
+}
+
 }  // namespace
+
+int launch_plan_patch(uint32_t* words, uint32_t n, const uint32_t* idx, const uint32_t* val, void* stream) {
+    if (n == 0) return hipSuccess;
+    if (n > kPatchWords) return hipErrorInvalidValue;
+    PatchArgs a;
+    a.words = words;
+    a.n = n;
+    for (uint32_t k = 0; k < n; ++k) {
+        a.idx[k] = idx[k];
+        a.val[k] = val[k];
+    }
+    hipLaunchKernelGGL(plan_patch_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), a);
+    return hipGetLastError();
+}
 
 int launch_write_pages(const uint32_t* ids, uint32_t n, const void* src, uint32_t src_dtype, uint8_t* data,
                        uint8_t* scales, uint32_t num_pages, uint32_t hkv, uint32_t d, uint32_t fmt,

@@ -239,6 +239,33 @@ dh_status dh_plan_create(dh_backend* backend, const dh_attn_config* cfg,
                          uint32_t flags, const dh_plan_options* options,
                          dh_plan** out);
 dh_status dh_plan_destroy(dh_plan* plan);
+
+/* Events of one decode step for dh_plan_update. */
+#define DH_PLAN_APPEND 0u        /* the sequence gained a page at the end      */
+#define DH_PLAN_REPLACE_LAST 1u  /* its last page was replaced (copy-on-write) */
+
+/* In-place update of a decode plan for the page-list changes one decode
+ * step makes: the events of TreeState::append_token (tree/state.rs:87-113),
+ * a new block on a block boundary (DH_PLAN_APPEND) and the copy-on-write of
+ * a shared last block (DH_PLAN_REPLACE_LAST, the cow_dst of
+ * dh_tree_append_token).  For k < n, event ops[k] applies page_ids[k] to
+ * sequence seqs[k] (its index in the plan's batch), in order.  Each
+ * sequence's last chunk is planned with room for 16 more pages; when every
+ * event fits, the plan's device tables are patched by one small kernel per
+ * 128 changed words on `stream` (ordered after earlier and before later
+ * dh_decode_batch calls on that stream; a decode on another stream must not
+ * overlap it) and *patched = 1.  When one does not fit (no room left, or a
+ * sequence without pages) nothing changes, *patched = 0, and the caller
+ * builds a new plan from the new page lists with dh_plan_create; forks (new
+ * sequences, newly shared runs) always take a new plan.  The patched plan
+ * reads exactly the pages the new lists hold and differs from a new plan
+ * only in how each sequence's last pages are cut into items (results equal
+ * within rounding).  Page ids must be inside the pool.  Not for prefill
+ * plans (DH_EUNSUPPORTED).  After DH_EHIP the plan's device tables may be
+ * partly patched: destroy it.  No counterpart in FlashInfer's plan / run
+ * split (batch_decode.rs:31-101), which re-plans every step. */
+dh_status dh_plan_update(dh_plan* plan, uint32_t n, const uint32_t* seqs, const uint32_t* ops,
+                         const uint32_t* page_ids, void* stream, uint32_t* patched);
 /* Workspace bytes dh_decode_batch needs with this plan
  * (cf. BatchDecodeKernel::workspace_size, batch_decode.rs:56-73). */
 size_t dh_plan_workspace_size(const dh_plan* plan);

@@ -1,0 +1,176 @@
+"""In-place plan updates (dh_plan_update) against the CPU oracle.
+
+A decode plan takes the page-list changes of a decode step without being
+rebuilt: a page appended to a sequence (TreeState::append_token on a block
+boundary, tree/state.rs:87-113) and the replacement of a shared partial last
+page by its copy-on-write copy.  Checked here:
+- TreeDecoder over a TreeState: a prompt, forks (also at a partial block, so
+  the next append copies on write), many steps of one token per leaf with
+  random K/V; every step's decode against the oracle (oracle_decode, pinned in
+  test_oracle.py) on the tree's block tables at that step; most steps patch
+  the plan, forks rebuild it;
+- the reserved room: 16 appends to one sequence fit, the 17th does not and
+  leaves the plan as it was;
+- argument errors, and prefill plans refused.
+Tolerance: 2e-2 beyond bf16 output rounding, as for every bf16 decode.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dendrite_amd import DhError, _lib
+from dendrite_amd.backend import (AttentionConfig, Backend, DecodePlan, Pool, PrefillPlan, TreeDecoder,
+                                  decode_batch)
+from dendrite_amd.cache import KvCache, KvCacheConfig, NodeId, TreeState
+from tests._helpers import TOL, excess_err
+
+pytestmark = pytest.mark.gpu
+
+HKV, D, HQ = 2, 64, 8
+
+
+class Mirror:
+    """The pool's bf16 pages on the host, for the oracle."""
+
+    def __init__(self, pool: Pool):
+        self.pool = pool
+        self.data = np.zeros((pool.num_pages, 2, HKV, 16, D), np.uint16)
+
+    def write(self, page, off, rng):
+        kv = torch.from_numpy(rng.standard_normal((2, HKV, 1, D)).astype(np.float32)).to(torch.bfloat16)
+        bits = kv.view(torch.int16).numpy().view(np.uint16)
+        self.pool.write_tokens(page, off, bits[0], bits[1])
+        self.data[page, :, :, off:off + 1] = bits
+
+    def copy(self, src, dst):
+        self.data[dst] = self.data[src]
+
+    def view(self):
+        n = self.pool.num_pages
+        return oracle.PoolView(np.arange(n, dtype=np.uint32), self.data.view(np.uint8).reshape(n, -1), None, n,
+                               _lib.KV_BF16, HKV, D)
+
+
+def _oracle(mirror, cfg, q, tables, lpl):
+    indptr = np.cumsum([0] + [len(t) for t in tables]).astype(np.uint32)
+    indices = np.array([b for t in tables for b in t], dtype=np.uint32)
+    return oracle.decode(mirror.view(), q.float().cpu().numpy(), _lib.DTYPE_F32, HQ, cfg.scale, cfg.gqa_mapping,
+                         indptr, indices, np.asarray(lpl, np.int32))
+
+
+def _q(rng, n):
+    return torch.from_numpy(rng.standard_normal((n, HQ, D)).astype(np.float32)).to(torch.bfloat16).to("cuda:0")
+
+
+def test_tree_decoder_patches_the_plan_step_after_step(backend):
+    rng = np.random.default_rng(11)
+    num_pages = 192
+    pool = Pool(backend, num_pages, HKV, D, _lib.KV_BF16)
+    mirror = Mirror(pool)
+    tree = TreeState(KvCache(KvCacheConfig(num_kv_heads=HKV, head_dim=D, max_blocks=num_pages)), 16)
+    cfg = AttentionConfig(HQ, HKV, D)
+    dec = TreeDecoder(backend, pool, tree, cfg, [NodeId.ROOT])
+
+    def append(i):
+        before = tree.get_block_table(dec.leaves[i]) or []
+        page, off = dec.append_token(i, int(rng.integers(0, 32000)))
+        after = tree.get_block_table(dec.leaves[i])
+        if before and after[-1] != before[-1] and len(after) == len(before):   # copy on write
+            mirror.copy(int(before[-1]), int(after[-1]))
+        mirror.write(page, off, rng)
+
+    def step():
+        q = _q(rng, len(dec.leaves))
+        out = dec.decode(q)
+        torch.cuda.synchronize()
+        ref = _oracle(mirror, cfg, q, dec.tables(), dec.last_page_len())
+        err = excess_err(out.float().cpu().numpy(), ref, _lib.DTYPE_BF16)
+        assert err <= TOL[_lib.DTYPE_BF16], f"step with {len(dec.leaves)} leaves: {err}"
+
+    for _ in range(37):                      # prompt: two full pages and five tokens
+        append(0)
+    step()
+    for _ in range(3):                       # forks at a partial block
+        dec.fork(0)
+    step()
+    for s in range(70):
+        for i in range(len(dec.leaves)):
+            append(i)
+            if (s + i) % 5 == 0:             # leaves drift apart in length
+                append(i)
+        if s in (9, 40):                     # a fork in the middle of decoding
+            dec.fork(1 + s % 3)
+        step()
+    assert dec.plans_built >= 4
+    assert dec.plans_patched >= 10, (dec.plans_built, dec.plans_patched)
+
+
+def _pages_plan(backend, pool, cfg, tables):
+    indptr = np.cumsum([0] + [len(t) for t in tables]).astype(np.uint32)
+    indices = np.array([b for t in tables for b in t], dtype=np.uint32)
+    return DecodePlan(backend, cfg, pool, indptr, indices)
+
+
+def _decode(plan, q, lpl):
+    out = torch.empty_like(q)
+    lp = torch.from_numpy(np.asarray(lpl, np.int32)).to("cuda:0")
+    decode_batch(plan, q, out, plan.workspace(), lp)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def test_room_for_sixteen_appends_then_a_new_plan(backend):
+    rng = np.random.default_rng(12)
+    pool = Pool(backend, 64, HKV, D, _lib.KV_BF16)
+    mirror = Mirror(pool)
+    for p in range(64):
+        for t in range(16):
+            mirror.write(p, t, rng)
+    cfg = AttentionConfig(HQ, HKV, D)
+    tables = [[0, 1, 2, 3], [0, 1, 5], [7]]
+    plan = _pages_plan(backend, pool, cfg, tables)
+    lpl = [16, 9, 3]
+    q = _q(rng, 3)
+    before = plan.stats()
+    for k in range(16):
+        assert plan.update([(0, _lib.PLAN_APPEND, 20 + k)])
+        tables[0].append(20 + k)
+    assert plan.stats()["total_pages"] == before["total_pages"] + 16
+    got = _decode(plan, q, lpl)
+    ref = _oracle(mirror, cfg, q, tables, lpl)
+    assert excess_err(got, ref, _lib.DTYPE_BF16) <= TOL[_lib.DTYPE_BF16]
+    # no room left: nothing changes, not even the events that would fit
+    assert not plan.update([(2, _lib.PLAN_APPEND, 40), (0, _lib.PLAN_APPEND, 41)])
+    assert np.array_equal(_decode(plan, q, lpl), got)
+    # the last page replaced (copy on write), in a batch with an append
+    assert plan.update([(1, _lib.PLAN_REPLACE_LAST, 44), (2, _lib.PLAN_APPEND, 45), (2, _lib.PLAN_APPEND, 46)])
+    tables[1][-1] = 44
+    tables[2] += [45, 46]
+    lpl = [16, 9, 12]
+    got = _decode(plan, q, lpl)
+    ref = _oracle(mirror, cfg, q, tables, lpl)
+    assert excess_err(got, ref, _lib.DTYPE_BF16) <= TOL[_lib.DTYPE_BF16]
+    # a new plan on the same lists agrees
+    fresh = _decode(_pages_plan(backend, pool, cfg, tables), q, lpl)
+    assert excess_err(fresh, ref, _lib.DTYPE_BF16) <= TOL[_lib.DTYPE_BF16]
+
+
+def test_update_errors(backend):
+    pool = Pool(backend, 16, HKV, D, _lib.KV_BF16)
+    cfg = AttentionConfig(HQ, HKV, D)
+    plan = _pages_plan(backend, pool, cfg, [[0, 1], [2], []])
+    for ev in ([(3, _lib.PLAN_APPEND, 4)], [(0, _lib.PLAN_APPEND, 16)], [(0, 7, 4)],
+               [(0, _lib.PLAN_APPEND, _lib.INVALID_PAGE)]):
+        with pytest.raises(DhError) as e:
+            plan.update(ev)
+        assert e.value.status == _lib.DH_EINVAL
+    assert plan.update([])                          # nothing to do
+    assert not plan.update([(2, _lib.PLAN_APPEND, 4)])   # a sequence without pages
+    pcfg = AttentionConfig(HQ, HKV, D)
+    pcfg.q_dtype = _lib.DTYPE_BF16
+    pre = PrefillPlan(backend, pcfg, pool, np.array([0, 2], np.uint32), np.array([0, 1], np.uint32),
+                      np.array([20], np.uint32), np.array([4], np.uint32), causal=True)
+    with pytest.raises(DhError) as e:
+        pre.update([(0, _lib.PLAN_APPEND, 3)])
+    assert e.value.status == _lib.DH_EUNSUPPORTED

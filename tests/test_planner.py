@@ -92,8 +92,33 @@ def test_c3_tree_reads_each_page_once_per_head():
     assert st["unique_pages"] == 1184 and st["page_reads"] == 1184
     assert st["total_pages"] == 64 * 536
     # every page id appears once in the plan's page list (per KV head the
-    # items of a chunk share that list)
-    assert Counter(plan["pages"].tolist()).most_common(1)[0][1] == 1
+    # items of a chunk share that list); the INVALID entries are the room
+    # reserved after each sequence's last chunk
+    ids = plan["pages"][plan["pages"] != INVALID]
+    assert len(ids) == 1184 and Counter(ids.tolist()).most_common(1)[0][1] == 1
+
+
+@pytest.mark.parametrize("name", ["c3_small", "c4_small", "c5_small"])
+def test_last_chunks_have_room_to_grow(name):
+    """Each sequence's last chunk is followed by 16 reserved (INVALID)
+    entries of the page list, which dh_plan_update fills in place; no other
+    item's pages reach into them."""
+    w = CASES[name]
+    plan = plan_inspect(_cfg(w), w.num_pool_pages, w.indptr, w.indices)
+    pages = plan["pages"]
+    reserved = set()
+    tails = set()
+    for it in plan["items"]:
+        if it["flags"] & 1:
+            end = it["page_off"] + it["npages"]
+            assert np.all(pages[end:end + 16] == INVALID), "no room after a last chunk"
+            reserved.update(range(end, end + 16))
+            tails.add(it["tail_seq"])
+    assert tails == set(range(w.batch))
+    for it in plan["items"]:
+        span = set(range(it["page_off"], it["page_off"] + it["npages"]))
+        assert not span & reserved
+    assert np.count_nonzero(pages == INVALID) == 16 * w.batch
 
 
 def test_tail_items_name_their_sequence():
