@@ -161,3 +161,14 @@ def test_rejects_bad_inputs():
     assert a["stats"] == plan_inspect(cfg, w.num_pool_pages, w.indptr, w.indices)["stats"]
     ip = np.array([0, 3, 2], dtype=np.uint32)
     assert _err(lambda: plan_inspect(cfg, w.num_pool_pages, ip, w.indices[:3])) == _lib.DH_EINVAL
+
+
+def test_sequence_length_limit():
+    """DH_MAX_SEQ_LEN tokens (8192 pages) plan; one page more is DH_EINVAL."""
+    cfg = AttentionConfig(8, 2, 128)
+    n = _lib.MAX_SEQ_LEN // 16
+    ok = plan_inspect(cfg, n + 1, np.array([0, n], np.uint32), np.arange(n, dtype=np.uint32))
+    assert ok["stats"]["total_pages"] == n
+    with pytest.raises(DhError) as e:
+        plan_inspect(cfg, n + 1, np.array([0, n + 1], np.uint32), np.arange(n + 1, dtype=np.uint32))
+    assert e.value.status == _lib.DH_EINVAL
