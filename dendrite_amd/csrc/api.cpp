@@ -137,6 +137,9 @@ struct dh_plan {
     // for dh_plan_update, and where items and pages start in dev (words).
     std::vector<uint32_t> tail_off, tail_n, tail_cap, tail_item_ptr, tail_items;
     size_t items_word, pages_word;
+    // Prefill plans with one partial state per row: the attention kernel
+    // writes out directly and there is no merge.
+    bool direct;
 };
 
 extern "C" {
@@ -595,6 +598,9 @@ static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh
         pl->tail_item_ptr = hp.tail_item_ptr;
         pl->tail_items = hp.tail_items;
     }
+    pl->direct = prefill;
+    for (uint32_t v = 0; prefill && v < batch; ++v)
+        if (hp.slot_ptr[v + 1] - hp.slot_ptr[v] != 1) pl->direct = false;
     pl->items_word = o_items / sizeof(uint32_t);
     pl->pages_word = o_pages / sizeof(uint32_t);
     retain(be);
@@ -801,11 +807,12 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
         a.n_wave_items = pl->n_wave_items;
         a.row_len = pl->row_len;
         a.item_lim = pl->item_lim;
+        a.out_direct = pl->direct ? out : nullptr;
         hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim,
                                                     pl->prefill, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     }
-    if (mask & 2u) {
+    if ((mask & 2u) && !pl->direct) {
         dh::MergeArgs m;
         m.slot_ptr = pl->slot_ptr;
         m.ws_o = ws_o;

@@ -1475,17 +1475,31 @@ __device__ __forceinline__ void dma_group_loop(const AttendArgs& a, const Item& 
 
 // Query rows of a wave's tiles in a DMA group item: tile rt of wave w covers
 // rows (rt * kWaves + w) * 16 .. +16.
-template <int D, int RT>
+template <int D, int RT, bool PF>
 __device__ __forceinline__ void write_partial_dma(const AttendArgs& a, const Item& it, int wave, int nrt,
-                                                  const uint32_t (&dst)[RT], const float (&m)[RT],
-                                                  const f4 (&L)[RT], const f4 (&O)[RT][D / 16], int g, int c) {
+                                                  const RowTargets<RT>& rtg, const float (&m)[RT],
+                                                  const f4 (&L)[RT], const f4 (&O)[RT][D / 16], int g, int c,
+                                                  bool f16) {
     constexpr int EPL = D / 16;
+    const uint32_t (&dst)[RT] = rtg.dst;
     #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         if (rt >= nrt) break;
         const uint32_t row = uint32_t(rt * kWaves + wave) * kTileRows + c;
         const float lt = L[rt][0];
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        if (PF && a.out_direct) {   // the row's only partial state is its output
+            if (row < it.nrows) {
+                uint8_t* o = static_cast<uint8_t*>(a.out_direct) + rtg.qoff[rt];
+                #pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const f4 v = O[rt][e] * inv;
+                    *reinterpret_cast<u32x2*>(o + 2 * (16 * e + 4 * g)) =
+                        u32x2{pack2(v[0], v[1], f16), pack2(v[2], v[3], f16)};
+                }
+            }
+            continue;
+        }
         float mx = 0.f;
         #pragma unroll
         for (int e = 0; e < EPL; ++e)
@@ -1534,7 +1548,7 @@ __device__ __forceinline__ void dma_group_run(const AttendArgs& a, const Item& i
         dma_group_loop<D, F16, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                   qB, rm, L, O);
     }
-    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
+    write_partial_dma<D, RT, PF>(a, it, wave, NRT, rtg, rm.m, L, O, g, c, F16);
 }
 
 // Item fields as wave-uniform values (they are: the item is the workgroup's),
@@ -1892,7 +1906,7 @@ __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& 
         dma8_group_loop<D, KVF, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                    qB, rm, L, O);
     }
-    write_partial_dma<D, RT>(a, it, wave, NRT, rtg.dst, rm.m, L, O, g, c);
+    write_partial_dma<D, RT, PF>(a, it, wave, NRT, rtg, rm.m, L, O, g, c, false);
 }
 
 template <int D, uint32_t KVF, bool PF>

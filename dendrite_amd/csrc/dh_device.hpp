@@ -110,6 +110,9 @@ struct AttendArgs {
     // and the group items' token ranges; null for decode plans.
     const uint32_t* row_len;
     const ItemLim* item_lim;
+    // Prefill plans whose every row has one partial state: the items write
+    // the normalised rows straight to out (no merge); null otherwise.
+    void* out_direct;
 };
 
 struct MergeArgs {

@@ -349,7 +349,9 @@ dh_status dh_decode_batch(dh_backend* backend, const dh_pool* pool,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* Stages of dh_decode_batch, for profiling: bit 0 = attention items,
- * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3. */
+ * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3.  A prefill
+ * plan in which every query row is one work item's (one partial state per
+ * row) has no merge: its attention stage writes out. */
 dh_status dh_decode_stages(dh_backend* backend, const dh_pool* pool,
                            const dh_plan* plan, const void* q,
                            const int32_t* last_page_len, void* out,
