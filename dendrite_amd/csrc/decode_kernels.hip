@@ -1571,7 +1571,7 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
                                                int c) {
     using C = DmaCfg<D>;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[C::RING];
-    __shared__ uint32_t ids[kGroupMaxPages];
+    __shared__ uint32_t ids[PF ? kPrefillMaxPages : kGroupMaxPages];
     const Item it = uniform_item(item);
     // Row targets, the last page's length and the page ids load together.
     RowTargets<C::RT> rtg;
@@ -1915,7 +1915,7 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
     using C = DmaCfg<D>;
     using C8 = Dma8Cfg<D>;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[C8::LDS];
-    __shared__ uint32_t ids[kGroupMaxPages];
+    __shared__ uint32_t ids[PF ? kPrefillMaxPages : kGroupMaxPages];
     const Item it = uniform_item(item);
     RowTargets<C::RT> rtg;
     dma_row_targets<D, C::RT>(a, it, wave, c, rtg);

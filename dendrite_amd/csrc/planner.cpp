@@ -431,6 +431,11 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     }
     out.num_group_items = uint32_t(gorder.size());
     out.num_wave_items = uint32_t(waves.size());
+    for (const Item& it : out.items)
+        if (it.npages > kMaxItemPages) {
+            err = "internal: an item of " + std::to_string(it.npages) + " pages";
+            return DH_EINVAL;
+        }
     // The items of each sequence's last chunk, by final item index.
     out.tail_item_ptr.assign(B + 1, 0);
     for (const Item& it : out.items)
@@ -519,11 +524,17 @@ int build_prefill_plan(const PrefillInput& in, HostPlan& out, std::string& err) 
             out.row_len[q_off[b] + i] = in.causal ? in.kv_len[b] - in.q_len[b] + i + 1 : in.kv_len[b];
     auto len_of = [&](uint32_t b, uint32_t i) { return out.row_len[q_off[b] + i]; };
 
-    // Chunk size: one chunk per block when blocks alone fill the chip.
+    // Chunk size: one chunk per block when blocks alone fill the chip, at
+    // most kPrefillMaxChunk pages: an item's page ids are staged in an LDS
+    // list of kPrefillMaxPages entries, and the last chunk of a block also
+    // takes the pages between its first and last query (at most
+    // tpb / 16 + 1 more).
+    const uint32_t kPrefillMaxChunk = uint32_t(kPrefillMaxPages) - (tpb + kPageSize - 1) / kPageSize - 1;
     uint64_t n_blocks = 0;
     for (uint32_t b = 0; b < B; ++b) n_blocks += (in.q_len[b] + tpb - 1) / tpb;
     uint32_t chunk = in.chunk_pages;
     if (!chunk) chunk = n_blocks * in.hkv >= 512 ? UINT32_MAX : 32;
+    chunk = std::min(chunk, kPrefillMaxChunk);
 
     // Blocks and their chunks: (sequence, token range, page range).
     struct Piece {
@@ -548,6 +559,11 @@ int build_prefill_plan(const PrefillInput& in, HostPlan& out, std::string& err) 
             }
         }
     }
+    for (const Piece& pc : pieces)
+        if (pc.p1 - pc.p0 > uint32_t(kPrefillMaxPages)) {
+            err = "internal: a prefill item of " + std::to_string(pc.p1 - pc.p0) + " pages";
+            return DH_EINVAL;
+        }
     // Partial slots: one per (chunk, query), contiguous per query.
     std::vector<uint32_t> count(nq, 0);
     for (const Piece& pc : pieces)

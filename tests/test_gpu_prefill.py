@@ -129,3 +129,14 @@ def test_hip_backend_prefill_matches_dense_causal_attention():
     ref = torch.softmax(s, -1) @ vd
     err = excess_err(out.float().cpu().numpy(), ref.numpy(), _lib.DTYPE_BF16)
     assert err <= TOL[_lib.DTYPE_BF16], err
+
+
+@pytest.mark.parametrize("chunk", [1000, 5000], ids=["chunk1000", "chunk5000"])
+def test_prefill_items_longer_than_decode_items(backend, chunk):
+    """Items of more than 256 pages (a prefill item's page-id list holds
+    2048), and a context longer than that, which the planner cuts into
+    chunks whatever chunk_pages asks for."""
+    _run(backend, 8, 2, 128, _lib.DTYPE_BF16, _lib.KV_BF16, kv_len=[5100, 4200], q_len=[100, 33],
+         chunk_pages=chunk, seed=11)
+    _run(backend, 4, 1, 128, _lib.DTYPE_BF16, _lib.KV_BF16, kv_len=[33000], q_len=[40], chunk_pages=chunk, seed=12)
+    _run(backend, 8, 2, 256, _lib.DTYPE_BF16, _lib.KV_MXFP8, kv_len=[6000], q_len=[20], chunk_pages=chunk, seed=13)
