@@ -533,7 +533,17 @@ int build_prefill_plan(const PrefillInput& in, HostPlan& out, std::string& err) 
     uint64_t n_blocks = 0;
     for (uint32_t b = 0; b < B; ++b) n_blocks += (in.q_len[b] + tpb - 1) / tpb;
     uint32_t chunk = in.chunk_pages;
-    if (!chunk) chunk = n_blocks * in.hkv >= 512 ? UINT32_MAX : 32;
+    if (!chunk && n_blocks * in.hkv >= 512) {
+        chunk = UINT32_MAX;
+    } else if (!chunk) {
+        // Fewer blocks than the chip holds: cut their pages into about 1024
+        // items (four per CU), at least 32 pages each.
+        uint64_t seen = 0;   // pages the blocks' last queries see
+        for (uint32_t b = 0; b < B; ++b)
+            for (uint32_t i0 = 0; i0 < in.q_len[b]; i0 += tpb)
+                seen += (len_of(b, std::min(in.q_len[b], i0 + tpb) - 1) + kPageSize - 1) / kPageSize;
+        chunk = uint32_t(std::max<uint64_t>(32, (seen * in.hkv + 1023) / 1024));
+    }
     chunk = std::min(chunk, kPrefillMaxChunk);
 
     // Blocks and their chunks: (sequence, token range, page range).
