@@ -2101,34 +2101,66 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     if (row >= a.batch * a.hq) return;
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
     const uint32_t s0 = a.slot_ptr[b], n = a.slot_ptr[b + 1] - s0;
-    float M = kNegInf;
-    for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh].lse);
-    M = wave_max(M);
     float acc[PL];
     #pragma unroll
     for (int k = 0; k < PL; ++k) acc[k] = 0.f;
     float W = 0.f;
-    if (M != kNegInf) {
-        for (uint32_t base = 0; base < n; base += 64) {
-            // Weight of slot base + lane, then the slots' O rows in groups of U.
-            const uint32_t k = base + lane;
-            const PartialLse pk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : PartialLse{kNegInf, 0.f};
+    if (n != 0 && n <= 64) {
+        // One pass: the log-sum-exps and the first U partial rows are loaded
+        // together (neither depends on the other), so a row with up to U
+        // partial states costs one memory round trip after slot_ptr.
+        const PartialLse pk = uint32_t(lane) < n ? a.ws_lse[uint64_t(s0 + lane) * a.hq + qh]
+                                                 : PartialLse{kNegInf, 0.f};
+        float v[U][PL];
+        #pragma unroll
+        for (int u = 0; u < U; ++u)
+            load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + min(uint32_t(u), n - 1)) * a.hq + qh) * D + lane * PL, v[u]);
+        const float M = wave_max(pk.lse);
+        if (M != kNegInf) {
             const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
-            W += wk;
+            W = wk;
             const float wo = __builtin_amdgcn_ldexpf(wk, int(pk.k));   // weight of the stored (scaled) O
-            const uint32_t cnt = min(64u, n - base);
-            for (uint32_t j0 = 0; j0 < cnt; j0 += U) {
-                float v[U][PL];
-                #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint32_t j = min(j0 + u, cnt - 1);
-                    load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL, v[u]);
+            for (uint32_t j0 = 0; j0 < n; j0 += U) {
+                if (j0) {
+                    #pragma unroll
+                    for (int u = 0; u < U; ++u)
+                        load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + min(j0 + u, n - 1)) * a.hq + qh) * D + lane * PL,
+                                              v[u]);
                 }
                 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const float w = (j0 + u < cnt) ? __shfl(wo, int(j0 + u), 64) : 0.f;
+                    const float w = (j0 + u < n) ? __shfl(wo, int(j0 + u), 64) : 0.f;
                     #pragma unroll
                     for (int q = 0; q < PL; ++q) acc[q] += w * v[u][q];
+                }
+            }
+        }
+    } else if (n > 64) {
+        float M = kNegInf;
+        for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh].lse);
+        M = wave_max(M);
+        if (M != kNegInf) {
+            for (uint32_t base = 0; base < n; base += 64) {
+                // Weight of slot base + lane, then the slots' O rows in groups of U.
+                const uint32_t k = base + lane;
+                const PartialLse pk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : PartialLse{kNegInf, 0.f};
+                const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
+                W += wk;
+                const float wo = __builtin_amdgcn_ldexpf(wk, int(pk.k));   // weight of the stored (scaled) O
+                const uint32_t cnt = min(64u, n - base);
+                for (uint32_t j0 = 0; j0 < cnt; j0 += U) {
+                    float v[U][PL];
+                    #pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const uint32_t j = min(j0 + u, cnt - 1);
+                        load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL, v[u]);
+                    }
+                    #pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const float w = (j0 + u < cnt) ? __shfl(wo, int(j0 + u), 64) : 0.f;
+                        #pragma unroll
+                        for (int q = 0; q < PL; ++q) acc[q] += w * v[u][q];
+                    }
                 }
             }
         }

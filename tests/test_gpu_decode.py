@@ -115,3 +115,11 @@ def test_empty_sequences(backend):
             if not t:
                 assert not np.any(got[b]), f"sequence {b} without pages is not zero"
         assert excess_err(got, run.reference(), w.q_dtype) <= TOL[w.q_dtype]
+
+
+def test_rows_with_many_partial_states(backend):
+    """One-page chunks: rows merge 70-150 partial states (the merge's general
+    path), beside rows with few (its one-pass path)."""
+    tables = [list(range(150)), list(range(70)) + [200, 201], [300], list(range(310, 330))]
+    w = workloads.custom(tables, 32, 8, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 400, last_page_len=[7, 16, 2, 11])
+    _check(w, backend, shared_chunk_pages=1, private_chunk_pages=1)
