@@ -320,7 +320,10 @@ dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages,
  * causal) and BatchPrefillKernel::run (flashinfer/batch_prefill.rs:86-101,
  * K/V written to pages first); chunked prefill over a cached context is
  * q_len < kv_len.  bf16 / f16 queries; FP8 / MXFP8 KV at head_dim 128 and
- * 256.  chunk_pages: KV pages per work item (0 = chosen from the work).
+ * 256.  chunk_pages: KV pages per work item (0 = chosen from the work:
+ * one item per block of queries when those fill the chip, else about 1024
+ * items); at most about 2040 whatever is asked (an item's page-id list
+ * holds 2048 entries), so longer contexts always take several items.
  * Host-side, synchronous. */
 dh_status dh_plan_create_prefill(dh_backend* backend, const dh_attn_config* cfg,
                                  const dh_pool* pool, const uint32_t* indptr,
