@@ -127,8 +127,10 @@ class TreeState:
             if b != INVALID:
                 self.pool.share(b)
         parent.num_children += 1
+        # state.rs:157-171: the walk stops at a parent that was collected
+        # (a released node with no children left, whose child lives on).
         depth, cur = 0, frm
-        while self.nodes[cur].parent is not None:
+        while cur in self.nodes and self.nodes[cur].parent is not None:
             depth += 1
             cur = self.nodes[cur].parent
         self.nodes[child.id] = child

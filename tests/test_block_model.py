@@ -633,3 +633,19 @@ def test_tree_matches_python_restatement(ops, max_blocks):
                 assert tree.get_node(n) is None
         for b in range(max_blocks):
             assert cache.pool.get_refcount(b) == rpool.refcount[b]
+
+
+def test_fork_below_a_collected_parent():
+    """Releasing a node and then its only child collects the parent while the
+    grandchild lives; a fork there counts depth up to the missing parent, as
+    calculate_depth does (tree/state.rs:157-171)."""
+    s, _ = _tree()
+    a = s.fork(NodeId.ROOT).node_id
+    b = s.fork(a).node_id
+    c = s.fork(b).node_id
+    s.release(a)
+    s.release(b)                      # a: inactive, no children left -> collected
+    assert s.get_node(a) is None and s.get_node(b) is not None
+    h = s.fork(b)
+    assert h.depth == 2
+    assert s.get_node(c).parent == b
