@@ -294,4 +294,14 @@ def random_tree(seed: int, hq: int, hkv: int, d: int, q_dtype: int, kv_format: i
                   name=f"tree{seed}", **kw)
 
 
-ALL = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}
+def c3prefix(seed: int = 0xC3) -> Workload:
+    """C3's shared-prefix stage alone: the 8192-token root shared by 64
+    leaves, each with one private page (MFMA counters of the prefix kernel
+    path without the tree's other levels)."""
+    w = c3(seed, root_pages=512, fanout=64, levels=1, level_pages=1)
+    w.name = "c3prefix"
+    w.description = "C3 root alone: 8192-token prefix shared by 64 leaves + 1 private page each, bf16, 32/8/128"
+    return w
+
+
+ALL = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5, "c3prefix": c3prefix}
