@@ -378,15 +378,23 @@ class TreeDecoder:
         self.tree = tree
         self.config = config
         self.leaves = [int(n) for n in leaves]
+        # Each leaf's last page (where its next token goes unless the tree
+        # allocates or copies a block), so an append reads no block table.
+        self._last = [self._table_last(n) for n in self.leaves]
         self._plan: Optional[DecodePlan] = None
         self._ws = None
         self._events: list[tuple[int, int, int]] = []
         self.plans_built = 0
         self.plans_patched = 0
 
+    def _table_last(self, node: int) -> int:
+        table = self.tree.get_block_table(node) or []
+        return int(table[-1]) if table else _lib.INVALID_PAGE
+
     def fork(self, i: int) -> int:
         """Forks leaf i into a new leaf (appended last); returns its index."""
         self.leaves.append(int(self.tree.fork(self.leaves[i]).node_id))
+        self._last.append(self._last[i])          # the child shares the parent's blocks
         self._plan = None
         return len(self.leaves) - 1
 
@@ -394,13 +402,14 @@ class TreeDecoder:
         node = self.leaves[i]
         n = self.tree.get_node(node).num_tokens
         cow = self.tree.append_token(node, token)
-        if cow is not None:
+        if n % _lib.PAGE_SIZE == 0:               # a new block at the end
+            self._last[i] = self._table_last(node)
+            self._events.append((i, _lib.PLAN_APPEND, self._last[i]))
+        elif cow is not None:                     # the shared last block copied
             self.pool.copy_page(int(cow[0]), int(cow[1]), stream)
-            self._events.append((i, _lib.PLAN_REPLACE_LAST, int(cow[1])))
-        table = self.tree.get_block_table(node)
-        if n % _lib.PAGE_SIZE == 0:
-            self._events.append((i, _lib.PLAN_APPEND, int(table[-1])))
-        return int(table[n // _lib.PAGE_SIZE]), n % _lib.PAGE_SIZE
+            self._last[i] = int(cow[1])
+            self._events.append((i, _lib.PLAN_REPLACE_LAST, self._last[i]))
+        return self._last[i], n % _lib.PAGE_SIZE
 
     def tables(self) -> list[list[int]]:
         return [[int(b) for b in self.tree.get_block_table(n)] for n in self.leaves]
