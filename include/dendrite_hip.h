@@ -262,7 +262,8 @@ dh_status dh_plan_destroy(dh_plan* plan);
  * only in how each sequence's last pages are cut into items (results equal
  * within rounding).  Page ids must be inside the pool.  Not for prefill
  * plans (DH_EUNSUPPORTED).  After DH_EHIP the plan's device tables may be
- * partly patched: destroy it.  No counterpart in FlashInfer's plan / run
+ * partly patched: destroy it.  Updates of one plan must not overlap each
+ * other on the host (the plan keeps host copies of its last chunks).  No counterpart in FlashInfer's plan / run
  * split (batch_decode.rs:31-101), which re-plans every step. */
 dh_status dh_plan_update(dh_plan* plan, uint32_t n, const uint32_t* seqs, const uint32_t* ops,
                          const uint32_t* page_ids, void* stream, uint32_t* patched);
