@@ -521,6 +521,38 @@ class HipBackend:
         self.pool.write_tokens(int(block), off, k, v)
         self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + k.shape[1])
 
+    def store_kv(self, block_id: int, key, value) -> None:
+        """ReferenceBackend::store_kv (backend.rs:140-143): the block's entry
+        becomes key / value ([1, num_kv_heads, n, head_dim], n <= 16), from
+        token 0 (overwrite, as the reference's map insert)."""
+        self.page_len.pop(int(block_id), None)
+        self._shadow.pop(int(block_id), None)
+        self.append_kv(key, value, BlockTable.from_blocks([int(block_id)]), 0)
+
+    def get_kv(self, block_id: int):
+        """ReferenceBackend::get_kv (backend.rs:135-138): the stored K and V of
+        a block as host tensors [1, num_kv_heads, n, head_dim] of the pool's
+        element type, or None when nothing is stored.  FP8 / MXFP8 pages hold
+        codes and scales (Pool.read_page), not elements: DH_EUNSUPPORTED."""
+        torch = _torch()
+        n = self.page_len.get(int(block_id), 0)
+        if n == 0:
+            return None
+        fmt = self.pool.kv_format
+        if fmt in (_lib.KV_FP8_E4M3, _lib.KV_MXFP8):
+            raise DhError(_lib.DH_EUNSUPPORTED, "FP8 / MXFP8 pages hold codes and scales: use Pool.read_page")
+        dt = {_lib.KV_F32: torch.float32, _lib.KV_BF16: torch.bfloat16, _lib.KV_F16: torch.float16}[fmt]
+        raw, _ = self.pool.read_page(int(block_id))
+        hkv, d = self.pool.num_kv_heads, self.pool.head_dim
+        t = torch.from_numpy(raw.copy()).view(dt).reshape(2, hkv, _lib.PAGE_SIZE, d)[:, :, :n]
+        return t[0:1].contiguous(), t[1:2].contiguous()
+
+    def clear_cache(self) -> None:
+        """ReferenceBackend::clear_cache (backend.rs:130-133): every stored
+        block is forgotten (decode then skips them, as blocks with no KV)."""
+        self.page_len.clear()
+        self._shadow.clear()
+
     def _csr(self, tables: Sequence[BlockTable]):
         indptr, indices, lpl = [0], [], []
         for t in tables:

@@ -7,6 +7,7 @@ CPU oracle on the same seeded inputs.
 """
 import numpy as np
 import pytest
+import torch
 
 import oracle
 from dendrite_amd import DhError, _lib
@@ -239,3 +240,28 @@ def test_fp8_block_scales_must_be_positive(backend, bad):
                           v_scale=np.ones(hkv, np.float32))
     _, s = pool.read_page(3)
     assert np.array_equal(s.view(np.float32), np.ones(2 * hkv, np.float32))
+
+
+def test_store_get_and_clear():
+    """store_kv / get_kv round trip (bf16 and f32 pools), overwrite
+    semantics, and clear_cache: afterwards decode sees no KV (zeros, as
+    ReferenceBackend with an empty cache, backend.rs:218-222)."""
+    for fmt, dt in ((_lib.KV_BF16, torch.bfloat16), (_lib.KV_F32, torch.float32)):
+        be = HipBackend(num_pages=8, num_kv_heads=2, head_dim=64, kv_format=fmt)
+        g = torch.Generator().manual_seed(5)
+        k = torch.randn(1, 2, 11, 64, generator=g).to(dt)
+        v = torch.randn(1, 2, 11, 64, generator=g).to(dt)
+        assert be.get_kv(3) is None
+        be.store_kv(3, k, v)
+        gk, gv = be.get_kv(3)
+        assert torch.equal(gk, k) and torch.equal(gv, v)
+        be.store_kv(3, k[:, :, :5], v[:, :, :5])            # overwrite: 5 tokens now
+        gk, gv = be.get_kv(3)
+        assert gk.shape[2] == 5 and torch.equal(gk, k[:, :, :5]) and torch.equal(gv, v[:, :, :5])
+        cfg = AttentionConfig(8, 2, 64)
+        cfg.q_dtype = _lib.DTYPE_BF16 if fmt == _lib.KV_BF16 else _lib.DTYPE_F32
+        q = torch.randn(1, 8, 1, 64, generator=g).to(dt)
+        assert be.decode(q, BlockTable.from_blocks([3]), cfg).abs().sum() > 0
+        be.clear_cache()
+        assert be.get_kv(3) is None
+        assert torch.count_nonzero(be.decode(q, BlockTable.from_blocks([3]), cfg)) == 0
