@@ -603,11 +603,14 @@ class HipBackend:
         query [B, num_heads, S, head_dim] over key / value [B, num_kv_heads,
         S, head_dim] (GQA per config), output like query.  As there, the block
         table is not read: K / V are staged in a temporary pool of the query's
-        dtype and run through a prefill plan (q_len = kv_len = S)."""
+        dtype and run through a prefill plan (q_len = kv_len = S).  float32
+        queries (the prefill kernel is 16-bit) run as a decode over one
+        virtual sequence per query, its page list cut after the query's own
+        token: the cascade plan reads the nested shared prefixes once."""
         torch = _torch()
         dev = f"cuda:{self.backend.device}"
-        if query.dtype not in (torch.bfloat16, torch.float16):
-            raise DhError(_lib.DH_EUNSUPPORTED, "prefill takes bf16 or f16 queries")
+        if query.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise DhError(_lib.DH_EUNSUPPORTED, "prefill takes float32, bf16 or f16 queries")
         bsz, hq, S, d = query.shape
         hkv = key.shape[1]
         if tuple(key.shape) != (bsz, hkv, S, d) or tuple(value.shape) != tuple(key.shape):
@@ -615,7 +618,7 @@ class HipBackend:
         if S == 0 or bsz == 0:
             return torch.zeros_like(query)
         npg = (S + _lib.PAGE_SIZE - 1) // _lib.PAGE_SIZE
-        fmt = _lib.KV_BF16 if query.dtype == torch.bfloat16 else _lib.KV_F16
+        fmt = {torch.bfloat16: _lib.KV_BF16, torch.float16: _lib.KV_F16, torch.float32: _lib.KV_F32}[query.dtype]
         pool = Pool(self.backend, bsz * npg, hkv, d, fmt)
         pad = npg * _lib.PAGE_SIZE - S
         kv = torch.stack([key, value], dim=1).to(dev, query.dtype)            # [B, 2, Hkv, S, D]
@@ -628,12 +631,24 @@ class HipBackend:
         cfg.gqa_mapping = config.gqa_mapping
         cfg.q_dtype = dtype_code(query.dtype)
         cfg.kv_format = fmt
+        q = query.to(dev).permute(0, 2, 1, 3).reshape(bsz * S, hq, d).contiguous()
+        out = torch.empty_like(q)
+        if fmt == _lib.KV_F32:
+            # query i of sequence b sees tokens 0 .. i: pages 0 .. i // 16 of
+            # b's, the last holding i % 16 + 1 of them
+            i = np.arange(S)
+            per = i // _lib.PAGE_SIZE + 1
+            indptr = np.concatenate([[0], np.cumsum(np.tile(per, bsz))]).astype(np.uint32)
+            indices = np.concatenate([b * npg + np.arange(n) for b in range(bsz) for n in per]).astype(np.uint32)
+            lpl = torch.from_numpy(np.tile(i % _lib.PAGE_SIZE + 1, bsz).astype(np.int32)).to(dev)
+            plan = DecodePlan(self.backend, cfg, pool, indptr, indices, cascade=True)
+            decode_batch(plan, q, out, plan.workspace(), lpl)
+            torch.cuda.synchronize(dev)
+            return out.reshape(bsz, S, hq, d).permute(0, 2, 1, 3).contiguous()
         indptr = np.arange(bsz + 1, dtype=np.uint32) * npg
         indices = np.arange(bsz * npg, dtype=np.uint32)
         lens = np.full(bsz, S, dtype=np.uint32)
         plan = PrefillPlan(self.backend, cfg, pool, indptr, indices, lens, lens, causal=True)
-        q = query.to(dev).permute(0, 2, 1, 3).reshape(bsz * S, hq, d).contiguous()
-        out = torch.empty_like(q)
         decode_batch(plan, q, out, plan.workspace())
         torch.cuda.synchronize(dev)
         return out.reshape(bsz, S, hq, d).permute(0, 2, 1, 3).contiguous()

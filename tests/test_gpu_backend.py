@@ -132,12 +132,12 @@ def test_backend_tree_decode_matches_oracle(kvf):
 
 
 def test_prefill_errors():
-    """prefill takes bf16 / f16 queries (f32: DH_EUNSUPPORTED) and key /
+    """prefill takes f32 / bf16 / f16 queries (else DH_EUNSUPPORTED) and key /
     value of the query's batch and length (else DH_EINVAL)."""
     import torch
     be = HipBackend(num_pages=4, num_kv_heads=4, head_dim=64)
     cfg = AttentionConfig(4, 4, 64)
-    q = torch.zeros(1, 4, 8, 64)
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.float64)
     with pytest.raises(DhError) as e:
         be.prefill(q, q, q, BlockTable(16), cfg)
     assert e.value.status == _lib.DH_EUNSUPPORTED

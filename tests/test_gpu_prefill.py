@@ -109,17 +109,20 @@ def test_prefill_long_context_many_items(backend):
     assert plan.stats()["num_items"] >= 8
 
 
-def test_hip_backend_prefill_matches_dense_causal_attention():
-    """HipBackend.prefill: the reference's dense causal prefill (tiled GQA)."""
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("S", [37, 300])
+def test_hip_backend_prefill_matches_dense_causal_attention(dt, S):
+    """HipBackend.prefill: the reference's dense causal prefill (tiled GQA);
+    float32 runs as a decode over per-query virtual sequences (1e-4)."""
     g = torch.Generator().manual_seed(4)
-    B, hq, hkv, S, d = 2, 8, 2, 37, 64
+    B, hq, hkv, d = 2, 8, 2, 64
     be = HipBackend(num_pages=16, num_kv_heads=hkv, head_dim=d)
-    q = torch.randn(B, hq, S, d, generator=g).to(torch.bfloat16)
-    k = torch.randn(B, hkv, S, d, generator=g).to(torch.bfloat16)
-    v = torch.randn(B, hkv, S, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, hq, S, d, generator=g).to(dt)
+    k = torch.randn(B, hkv, S, d, generator=g).to(dt)
+    v = torch.randn(B, hkv, S, d, generator=g).to(dt)
     cfg = AttentionConfig(hq, hkv, d)
     out = be.prefill(q, k, v, None, cfg)
-    assert tuple(out.shape) == (B, hq, S, d) and out.dtype == torch.bfloat16
+    assert tuple(out.shape) == (B, hq, S, d) and out.dtype == dt
     # f64 dense causal attention on the same (bf16) inputs
     qd, kd, vd = (x.double() for x in (q, k, v))
     kd = kd.repeat(1, hq // hkv, 1, 1)
@@ -127,8 +130,9 @@ def test_hip_backend_prefill_matches_dense_causal_attention():
     s = qd @ kd.transpose(2, 3) * cfg.scale
     s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
     ref = torch.softmax(s, -1) @ vd
-    err = excess_err(out.float().cpu().numpy(), ref.numpy(), _lib.DTYPE_BF16)
-    assert err <= TOL[_lib.DTYPE_BF16], err
+    code = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
+    err = excess_err(out.float().cpu().numpy(), ref.numpy(), code)
+    assert err <= TOL[code], err
 
 
 @pytest.mark.parametrize("chunk", [1000, 5000], ids=["chunk1000", "chunk5000"])
