@@ -265,3 +265,46 @@ def test_store_get_and_clear():
         be.clear_cache()
         assert be.get_kv(3) is None
         assert torch.count_nonzero(be.decode(q, BlockTable.from_blocks([3]), cfg)) == 0
+
+
+# ------------------------- the reference's own backend tests (backend.rs:346-415)
+def test_reference_backend_new():
+    backend = HipBackend.new(num_pages=4, num_kv_heads=4, head_dim=64)
+    assert backend.page_len == {}
+
+
+def test_reference_backend_store_kv():
+    import torch
+    backend = HipBackend.new(num_pages=4, num_kv_heads=4, head_dim=64, kv_format=_lib.KV_F32)
+    key = torch.randn(1, 4, 16, 64)
+    value = torch.randn(1, 4, 16, 64)
+    backend.store_kv(0, key, value)
+    assert backend.get_kv(0) is not None
+
+
+def test_reference_backend_clear_cache():
+    import torch
+    backend = HipBackend.new(num_pages=4, num_kv_heads=4, head_dim=64, kv_format=_lib.KV_F32)
+    backend.store_kv(0, torch.randn(1, 4, 16, 64), torch.randn(1, 4, 16, 64))
+    assert backend.page_len
+    backend.clear_cache()
+    assert not backend.page_len
+
+
+def test_reference_backend_prefill():
+    import torch
+    backend = HipBackend.new(num_pages=4, num_kv_heads=4, head_dim=64)
+    config = AttentionConfig(4, 4, 64)
+    query, key, value = (torch.randn(1, 4, 8, 64) for _ in range(3))
+    output = backend.prefill(query, key, value, BlockTable(16), config)
+    assert tuple(output.shape) == tuple(query.shape)
+
+
+def test_reference_backend_prefill_gqa():
+    import torch
+    backend = HipBackend.new(num_pages=4, num_kv_heads=2, head_dim=64)
+    config = AttentionConfig(8, 2, 64)
+    query = torch.randn(1, 8, 4, 64)
+    key, value = torch.randn(1, 2, 4, 64), torch.randn(1, 2, 4, 64)
+    output = backend.prefill(query, key, value, BlockTable(16), config)
+    assert tuple(output.shape) == tuple(query.shape)
