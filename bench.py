@@ -218,8 +218,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path "
-                                   "shards by tree / KV head across GPUs, see DESIGN.md)"}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (across GPUs "
+                                   "the path would shard by tree or by KV head, with no kernel change)"}))
         sys.exit(2)
 
     import torch
