@@ -257,6 +257,26 @@ class DecodePlan:
                                    C.byref(opt), C.byref(self._h)))
         self.workspace_size = lib().dh_plan_workspace_size(self._h)
 
+    @classmethod
+    def from_tree(cls, backend: Backend, config: AttentionConfig, pool: Pool, tree, nodes,
+                  cascade: bool = True) -> "DecodePlan":
+        """dh_plan_create_tree: a plan over tree nodes, their page lists read
+        from the tree's block tables by the library."""
+        self = cls.__new__(cls)
+        self.backend, self.pool, self.config = backend, pool, config
+        ns = np.ascontiguousarray(nodes, dtype=np.uint64)
+        self.batch_size = len(ns)
+        self._c = config.to_c()
+        self._h = C.c_void_p()
+        self._destroy = lib().dh_plan_destroy
+        opt = _lib.dh_plan_options()
+        check(lib().dh_plan_create_tree(backend._h, C.byref(self._c), pool._h, tree._h,
+                                        ns.ctypes.data_as(_lib._PU64), len(ns),
+                                        _lib.PLAN_CASCADE if cascade else _lib.PLAN_FLAT,
+                                        C.byref(opt), C.byref(self._h)))
+        self.workspace_size = lib().dh_plan_workspace_size(self._h)
+        return self
+
     def __del__(self):
         # Bound at construction: module globals may already be gone when an
         # object is collected at interpreter shutdown.
@@ -415,7 +435,11 @@ class TreeDecoder:
         return [[int(b) for b in self.tree.get_block_table(n)] for n in self.leaves]
 
     def last_page_len(self) -> np.ndarray:
-        return np.array([self.tree.get_node(n).num_tokens % _lib.PAGE_SIZE for n in self.leaves], np.int32)
+        ns = np.ascontiguousarray(self.leaves, dtype=np.uint64)
+        out = np.zeros(len(ns), np.int32)
+        check(lib().dh_tree_last_page_len(self.tree._h, ns.ctypes.data_as(_lib._PU64), len(ns),
+                                          out.ctypes.data_as(C.POINTER(C.c_int32))))
+        return out
 
     def decode(self, q, out=None, stream=None):
         torch = _torch()
@@ -426,10 +450,7 @@ class TreeDecoder:
                 self._plan = None
         self._events = []
         if self._plan is None:
-            tables = self.tables()
-            indptr = np.cumsum([0] + [len(t) for t in tables]).astype(np.uint32)
-            indices = np.array([b for t in tables for b in t], dtype=np.uint32)
-            self._plan = DecodePlan(self.backend, self.config, self.pool, indptr, indices)
+            self._plan = DecodePlan.from_tree(self.backend, self.config, self.pool, self.tree, self.leaves)
             self._ws = self._plan.workspace()
             self.plans_built += 1
         dev = f"cuda:{self.backend.device}"

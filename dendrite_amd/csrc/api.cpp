@@ -629,6 +629,38 @@ dh_status dh_plan_create(dh_backend* be, const dh_attn_config* cfg, const dh_poo
     return upload_plan(be, cfg, pool, hp, batch, false, out);
 }
 
+dh_status dh_plan_create_tree(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
+                              const dh_tree* tree, const uint64_t* nodes, uint32_t n, uint32_t flags,
+                              const dh_plan_options* opt, dh_plan** out) {
+    if (!tree || !out || (n && !nodes)) return fail(DH_EINVAL, "NULL argument");
+    *out = nullptr;
+    std::vector<uint32_t> indptr(1, 0), indices;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t cnt = 0, got = 0;
+        dh_status st = dh_tree_get_block_table(tree, nodes[i], nullptr, 0, &cnt);
+        if (st != DH_OK) return st;
+        const size_t o = indices.size();
+        indices.resize(o + cnt);
+        st = dh_tree_get_block_table(tree, nodes[i], indices.data() + o, cnt, &got);
+        if (st != DH_OK) return st;
+        if (got != cnt) return fail(DH_EINVAL, "node %llu changed while it was read", (unsigned long long)nodes[i]);
+        indptr.push_back(uint32_t(indices.size()));
+    }
+    return dh_plan_create(be, cfg, pool, indptr.data(), indices.empty() ? nullptr : indices.data(), n, flags,
+                          opt, out);
+}
+
+dh_status dh_tree_last_page_len(const dh_tree* tree, const uint64_t* nodes, uint32_t n, int32_t* out) {
+    if (!tree || (n && (!nodes || !out))) return fail(DH_EINVAL, "NULL argument");
+    for (uint32_t i = 0; i < n; ++i) {
+        dh_node_info info;
+        const dh_status st = dh_tree_get_node(tree, nodes[i], &info);
+        if (st != DH_OK) return st;
+        out[i] = int32_t(info.num_tokens % DH_PAGE_SIZE);
+    }
+    return DH_OK;
+}
+
 dh_status dh_plan_create_prefill(dh_backend* be, const dh_attn_config* cfg, const dh_pool* pool,
                                  const uint32_t* indptr, const uint32_t* indices, const uint32_t* kv_len,
                                  const uint32_t* q_len, uint32_t batch, uint32_t causal, uint32_t chunk_pages,

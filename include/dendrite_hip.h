@@ -478,6 +478,19 @@ dh_status dh_tree_get_tokens(const dh_tree* tree, uint64_t node, uint32_t* token
                              uint32_t cap, uint32_t* n);
 uint32_t dh_tree_num_nodes(const dh_tree* tree);
 
+/* The cascade planner wired to TreeState: a decode plan over tree nodes (the
+ * leaves being decoded), their page lists read from the tree's block tables
+ * (TreeState::get_block_table, tree/state.rs:149-154) in one call, so the
+ * caller assembles no CSR arrays.  Otherwise dh_plan_create with flags /
+ * options; sequence i of the plan is nodes[i].  Trees of 16-token blocks. */
+dh_status dh_plan_create_tree(dh_backend* backend, const dh_attn_config* cfg, const dh_pool* pool,
+                              const dh_tree* tree, const uint64_t* nodes, uint32_t n, uint32_t flags,
+                              const dh_plan_options* options, dh_plan** out);
+/* last_page_len of each node for dh_decode_batch: its token count mod 16
+ * (0 for a full last page, as PageTable::last_page_len reports it,
+ * cache/paged.rs:384-390).  Host array of n entries. */
+dh_status dh_tree_last_page_len(const dh_tree* tree, const uint64_t* nodes, uint32_t n, int32_t* out);
+
 /* ------------------------------------- synthetic inputs (tests, benchmarks) */
 
 /* No counterpart in the reference: seeded generators for the benchmark

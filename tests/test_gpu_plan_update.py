@@ -174,3 +174,39 @@ def test_update_errors(backend):
     with pytest.raises(DhError) as e:
         pre.update([(0, _lib.PLAN_APPEND, 3)])
     assert e.value.status == _lib.DH_EUNSUPPORTED
+
+
+def test_plan_from_tree_equals_plan_from_its_tables(backend):
+    """dh_plan_create_tree reads the same page lists a caller would pass in
+    CSR form (outputs bit-identical), and dh_tree_last_page_len is each
+    node's token count mod 16."""
+    rng = np.random.default_rng(13)
+    pool = Pool(backend, 96, HKV, D, _lib.KV_BF16)
+    mirror = Mirror(pool)
+    tree = TreeState(KvCache(KvCacheConfig(num_kv_heads=HKV, head_dim=D, max_blocks=96)), 16)
+    cfg = AttentionConfig(HQ, HKV, D)
+    dec = TreeDecoder(backend, pool, tree, cfg, [NodeId.ROOT])
+    def append(i):
+        before = tree.get_block_table(dec.leaves[i]) or []
+        page, off = dec.append_token(i, 2)
+        after = tree.get_block_table(dec.leaves[i])
+        if before and len(after) == len(before) and after[-1] != before[-1]:   # copy on write
+            mirror.copy(int(before[-1]), int(after[-1]))
+        mirror.write(page, off, rng)
+
+    for _ in range(40):
+        append(0)
+    for _ in range(3):
+        dec.fork(0)
+    for i in range(1, 4):
+        for _ in range(5 * i + 7):
+            append(i)
+    lpl = dec.last_page_len()
+    assert list(lpl) == [tree.get_node(n).num_tokens % 16 for n in dec.leaves]
+    q = _q(rng, len(dec.leaves))
+    from dendrite_amd.backend import DecodePlan as DP
+    a = _decode(DP.from_tree(backend, cfg, pool, tree, dec.leaves), q, lpl)
+    b = _decode(_pages_plan(backend, pool, cfg, dec.tables()), q, lpl)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref = _oracle(mirror, cfg, q, dec.tables(), lpl)
+    assert excess_err(a, ref, _lib.DTYPE_BF16) <= TOL[_lib.DTYPE_BF16]
