@@ -159,6 +159,39 @@ def bench_prefill(args):
                       "steps": args.steps, "warmup": args.warmup}), flush=True)
 
 
+def bench_plan_timing(args):
+    """Host cost of keeping a decode plan current: dh_plan_create (planning
+    and upload) against dh_plan_update with one appended page for each of
+    32 sequences (the events of a decode step), medians."""
+    import time
+    import torch
+    from dendrite_amd import _lib, workloads
+    from dendrite_amd.backend import Backend, DecodePlan, Pool
+    be = Backend(0)
+    w = workloads.ALL[args.workload]()
+    pool = Pool(be, w.num_pool_pages, w.hkv, w.d, w.kv_format)
+    cfg = w.attention_config()
+    t_create = []
+    for _ in range(7):
+        t0 = time.perf_counter()
+        plan = DecodePlan(be, cfg, pool, w.indptr, w.indices)
+        t_create.append(time.perf_counter() - t0)
+    n_ev = min(32, w.batch)
+    t_update, patched = [], 0
+    for k in range(16):          # 16 rounds: every sequence keeps room for its appends
+        seqs = [(k * n_ev + j) % w.batch for j in range(n_ev)]
+        ev = [(b, _lib.PLAN_APPEND, int(w.indices[w.indptr[b]])) for b in seqs]
+        t0 = time.perf_counter()
+        patched += plan.update(ev)
+        t_update.append(time.perf_counter() - t0)
+    torch.cuda.synchronize()
+    print(json.dumps({"metric": "decode plan upkeep (host)", "workload": w.name,
+                      "create_us": round(1e6 * float(np.median(t_create)), 1),
+                      "update_us": round(1e6 * float(np.median(t_update)), 1),
+                      "update_events": n_ev, "patched": patched, "rounds": len(t_update),
+                      "note": "update through the Python binding; create includes the plan upload"}))
+
+
 def bench_write(args):
     """Quantise-on-write throughput: N bf16 pages [2][Hkv][16][D] resident in
     HBM into a pool of the workload's shape and format, through
@@ -206,6 +239,8 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--plan-timing", action="store_true",
+                    help="only time dh_plan_create against dh_plan_update (32 appended pages) on the host")
     ap.add_argument("--prefill", default="", metavar="CTX:NEW[xB]",
                     help="only measure paged causal prefill: NEW query tokens after CTX cached tokens, "
                          "B sequences, at the workload's head shape and KV format (e.g. 0:4096, 8192:2048x4)")
@@ -236,6 +271,9 @@ def main():
 
     from dendrite_amd.backend import Backend, DecodePlan, Pool, decode_batch, raw_to_tensor
 
+    if args.plan_timing:
+        bench_plan_timing(args)
+        return
     if args.write_pages:
         bench_write(args)
         return
