@@ -119,10 +119,12 @@ __global__ __launch_bounds__(256) void write_pages_kernel(WriteArgs w) {
     const uint32_t per_page = 2 * w.hkv;
     if (blk >= w.n * per_page) return;
     const uint32_t i = blk / per_page, ph = blk - i * per_page;
-    const uint32_t pid = w.ids[i];
-    if (pid >= w.num_pages) return;
+    // The source block does not depend on the page id: both loads go out
+    // together, so a block costs one memory round trip before its stores.
     float x[E];
     load_src<SRC, E>(w.src, uint64_t(blk) * 16 * D + uint64_t(lane) * E, x);
+    const uint32_t pid = w.ids[i];
+    if (pid >= w.num_pages) return;
     const uint64_t dblk = uint64_t(pid) * per_page + ph;   // destination block
     const uint64_t de = dblk * 16 * D + uint64_t(lane) * E;
     if constexpr (FMT == kF32) {
