@@ -154,6 +154,7 @@ SIGNATURES = {
     "dh_tree_get_block_table": (_I, [_P, _U64, _PU32, _U32, _PU32]),
     "dh_tree_get_tokens": (_I, [_P, _U64, _PU32, _U32, _PU32]),
     "dh_tree_num_nodes": (_U32, [_P]),
+    "dh_tree_tokens_per_block": (_U32, [_P]),
     "dh_plan_create_tree": (_I, [_P, C.POINTER(dh_attn_config), _P, _P, _PU64, _U32, _U32,
                                  C.POINTER(dh_plan_options), C.POINTER(_P)]),
     "dh_tree_last_page_len": (_I, [_P, _PU64, _U32, C.POINTER(C.c_int32)]),

@@ -50,6 +50,17 @@ def raw_to_tensor(raw: np.ndarray, q_dtype: int, device: str = "cuda:0"):
     return t.view(torch.bfloat16 if q_dtype == _lib.DTYPE_BF16 else torch.float16).to(device)
 
 
+def _as_torch_stream(stream):
+    """torch stream object for a stream argument (None: the current stream;
+    an int: a raw hipStream_t handle)."""
+    torch = _torch()
+    if stream is None:
+        return torch.cuda.current_stream()
+    if isinstance(stream, int):
+        return torch.cuda.ExternalStream(stream)
+    return stream
+
+
 def _stream_ptr(stream) -> Optional[int]:
     if stream is None:
         torch = _torch()
@@ -393,6 +404,10 @@ class TreeDecoder:
     sequences, in order; q / out are device tensors [leaves][Hq][D]."""
 
     def __init__(self, backend: Backend, pool: Pool, tree, config: AttentionConfig, leaves):
+        if tree.tokens_per_block != _lib.PAGE_SIZE:
+            raise DhError(_lib.DH_EUNSUPPORTED,
+                          f"TreeDecoder needs a tree of {_lib.PAGE_SIZE}-token blocks "
+                          f"(this one has {tree.tokens_per_block})")
         self.backend = backend
         self.pool = pool
         self.tree = tree
@@ -404,6 +419,7 @@ class TreeDecoder:
         self._plan: Optional[DecodePlan] = None
         self._ws = None
         self._events: list[tuple[int, int, int]] = []
+        self._lpl = None    # last decode's device last_page_len, alive until the next decode
         self.plans_built = 0
         self.plans_patched = 0
 
@@ -454,10 +470,14 @@ class TreeDecoder:
             self._ws = self._plan.workspace()
             self.plans_built += 1
         dev = f"cuda:{self.backend.device}"
-        lpl = torch.from_numpy(self.last_page_len()).to(dev)   # 0 reads as a full page
         if out is None:
             out = torch.empty_like(q)
-        decode_batch(self._plan, q, out, self._ws, lpl, stream)
+        # The lengths are copied on the decode's stream and kept on self until
+        # the next decode: the caching allocator cannot hand their memory to
+        # another tensor while the kernels may still read it.
+        with torch.cuda.stream(_as_torch_stream(stream)):
+            self._lpl = torch.from_numpy(self.last_page_len()).to(dev)   # 0 reads as a full page
+        decode_batch(self._plan, q, out, self._ws, self._lpl, stream)
         return out
 
 
@@ -531,6 +551,16 @@ class HipBackend:
         if block is None or not block.is_valid():
             return                                   # backend.rs:296-298: no block, no store
         off = position % _lib.PAGE_SIZE
+        stored = self.page_len.get(int(block), 0)
+        if off > stored:
+            # Tokens [stored, off) of the page were never written (a fresh
+            # page, or one forgotten by clear_cache): attending to them would
+            # read zeros or stale K/V.  The reference's store keeps only the
+            # given tokens (backend.rs:285-301); writes here go to their
+            # offset, so the page must be filled from the front.
+            raise DhError(_lib.DH_EUNSUPPORTED,
+                          f"append_kv at position {position}: block {int(block)} holds {stored} tokens, "
+                          f"so offset {off} would leave tokens {stored}..{off - 1} unwritten")
         if self.pool.kv_format in (_lib.KV_FP8_E4M3, _lib.KV_MXFP8):
             n = self._append_quantised(int(block), off, key, value)
             self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + n)

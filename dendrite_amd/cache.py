@@ -290,6 +290,10 @@ class TreeState:
     def num_nodes(self) -> int:
         return lib().dh_tree_num_nodes(self._h)
 
+    @property
+    def tokens_per_block(self) -> int:
+        return lib().dh_tree_tokens_per_block(self._h)
+
 
 __all__ = ["BlockId", "NodeId", "BlockTable", "BlockPool", "KvCacheConfig", "KvCache",
            "ForkHandle", "NodeInfo", "TreeState", "DhError"]

@@ -634,6 +634,9 @@ dh_status dh_plan_create_tree(dh_backend* be, const dh_attn_config* cfg, const d
                               const dh_plan_options* opt, dh_plan** out) {
     if (!tree || !out || (n && !nodes)) return fail(DH_EINVAL, "NULL argument");
     *out = nullptr;
+    if (dh_tree_tokens_per_block(tree) != DH_PAGE_SIZE)
+        return fail(DH_EUNSUPPORTED, "the tree has %u-token blocks; decode pages hold %u tokens",
+                    dh_tree_tokens_per_block(tree), DH_PAGE_SIZE);
     std::vector<uint32_t> indptr(1, 0), indices;
     for (uint32_t i = 0; i < n; ++i) {
         uint32_t cnt = 0, got = 0;
@@ -652,6 +655,9 @@ dh_status dh_plan_create_tree(dh_backend* be, const dh_attn_config* cfg, const d
 
 dh_status dh_tree_last_page_len(const dh_tree* tree, const uint64_t* nodes, uint32_t n, int32_t* out) {
     if (!tree || (n && (!nodes || !out))) return fail(DH_EINVAL, "NULL argument");
+    if (dh_tree_tokens_per_block(tree) != DH_PAGE_SIZE)
+        return fail(DH_EUNSUPPORTED, "the tree has %u-token blocks; decode pages hold %u tokens",
+                    dh_tree_tokens_per_block(tree), DH_PAGE_SIZE);
     for (uint32_t i = 0; i < n; ++i) {
         dh_node_info info;
         const dh_status st = dh_tree_get_node(tree, nodes[i], &info);
@@ -792,9 +798,28 @@ dh_status dh_plan_get_stats(const dh_plan* pl, dh_plan_stats* st) {
 
 /* ------------------------------------------------------------------ decode */
 
-dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
-                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
-                           uint32_t mask, void* stream) {
+// The decode kernels dereference q, out, the workspace and last_page_len on
+// the device; a pageable host pointer there would fault the GPU, so each is
+// checked once per thread and then remembered (a few recently seen device
+// pointers; the check costs a runtime query only for a new pointer).
+static dh_status check_device_ptr(const void* p, const char* what) {
+    thread_local const void* seen[8] = {};
+    thread_local unsigned next = 0;
+    for (const void* s : seen)
+        if (s == p) return DH_OK;
+    hipPointerAttribute_t attr;
+    const hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess || attr.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        return fail(DH_EINVAL, "%s is not GPU-accessible memory (copy a host array to the device first)", what);
+    }
+    seen[next++ % 8] = p;
+    return DH_OK;
+}
+
+static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                             const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes, uint32_t mask,
+                             void* stream) {
     if (!be || !pool || !pl) return fail(DH_EINVAL, "NULL argument");
     if (pl->be != be || pool->be != be) return fail(DH_EINVAL, "plan/pool belong to another backend");
     if (pool->num_pages != pl->pool_pages || pool->hkv != pl->cfg.num_kv_heads ||
@@ -809,6 +834,13 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
                     ws_bytes, pl->ws_bytes);
     if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
     DH_DEVICE(be->device);
+    for (const auto& [ptr, what] : {std::pair<const void*, const char*>{q, "q"}, {out, "out"},
+                                    {pl->ws_bytes ? ws : nullptr, "workspace"},
+                                    {last_page_len, "last_page_len"}}) {
+        if (!ptr) continue;
+        const dh_status st = check_device_ptr(ptr, what);
+        if (st != DH_OK) return st;
+    }
     const dh_attn_config& c = pl->cfg;
     // Group items address query rows by 32-bit byte offsets into q.
     if (uint64_t(pl->batch) * c.num_heads * c.head_dim * (c.q_dtype == DH_DTYPE_F32 ? 4u : 2u) > 0xFFFFFFFFull)
@@ -858,10 +890,16 @@ dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* p
     return DH_OK;
 }
 
+dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
+                           uint32_t mask, void* stream) {
+    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, mask, stream);
+}
+
 dh_status dh_decode_batch(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
                           void* stream) {
-    return dh_decode_stages(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream);
+    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream);
 }
 
 /* ------------------------------------------------------------------- merge */

@@ -390,4 +390,6 @@ uint32_t dh_tree_num_nodes(const dh_tree* t) {
     return uint32_t(t->nodes.size());
 }
 
+uint32_t dh_tree_tokens_per_block(const dh_tree* t) { return t ? t->tokens_per_block : 0u; }
+
 }  // extern "C"

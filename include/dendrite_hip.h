@@ -343,7 +343,10 @@ dh_status dh_plan_create_prefill(dh_backend* backend, const dh_attn_config* cfg,
  *   last_page_len : device int32[batch] or NULL (all pages full).  Tokens in
  *                   each sequence's last page, 1..16.  0 is read as a full
  *                   page, the value PageTable::last_page_len reports for one
- *                   (cache/paged.rs:384-390).
+ *                   (cache/paged.rs:384-390).  Must be GPU-accessible memory
+ *                   (a host array, e.g. from dh_tree_last_page_len, is copied
+ *                   to the device first); q, out, the workspace and it are
+ *                   checked and a pageable host pointer is DH_EINVAL.
  *   workspace     : device, >= dh_plan_workspace_size(plan) bytes.
  * Replaces BatchDecodeKernel::run (batch_decode.rs:86-101) and
  * CascadeAttention::run (cascade.rs:84-101).  Allocates nothing. */
@@ -477,18 +480,26 @@ dh_status dh_tree_get_block_table(const dh_tree* tree, uint64_t node, uint32_t* 
 dh_status dh_tree_get_tokens(const dh_tree* tree, uint64_t node, uint32_t* tokens,
                              uint32_t cap, uint32_t* n);
 uint32_t dh_tree_num_nodes(const dh_tree* tree);
+/* Tokens per block of the tree (TreeState's tokens_per_block, tree/state.rs:
+ * 29-45; 0 for NULL).  The decode path reads 16-token pages, so the tree
+ * entry points below take trees of DH_PAGE_SIZE-token blocks only. */
+uint32_t dh_tree_tokens_per_block(const dh_tree* tree);
 
 /* The cascade planner wired to TreeState: a decode plan over tree nodes (the
  * leaves being decoded), their page lists read from the tree's block tables
  * (TreeState::get_block_table, tree/state.rs:149-154) in one call, so the
  * caller assembles no CSR arrays.  Otherwise dh_plan_create with flags /
- * options; sequence i of the plan is nodes[i].  Trees of 16-token blocks. */
+ * options; sequence i of the plan is nodes[i].  DH_EUNSUPPORTED for a tree
+ * whose blocks are not DH_PAGE_SIZE tokens (a page holds 16 tokens). */
 dh_status dh_plan_create_tree(dh_backend* backend, const dh_attn_config* cfg, const dh_pool* pool,
                               const dh_tree* tree, const uint64_t* nodes, uint32_t n, uint32_t flags,
                               const dh_plan_options* options, dh_plan** out);
 /* last_page_len of each node for dh_decode_batch: its token count mod 16
  * (0 for a full last page, as PageTable::last_page_len reports it,
- * cache/paged.rs:384-390).  Host array of n entries. */
+ * cache/paged.rs:384-390).  `out` is a HOST array of n entries:
+ * dh_decode_batch reads last_page_len from device memory, so copy it there
+ * first (hipMemcpyAsync on the decode's stream).  DH_EUNSUPPORTED for a tree
+ * whose blocks are not DH_PAGE_SIZE tokens. */
 dh_status dh_tree_last_page_len(const dh_tree* tree, const uint64_t* nodes, uint32_t n, int32_t* out);
 
 /* ------------------------------------- synthetic inputs (tests, benchmarks) */

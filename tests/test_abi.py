@@ -122,3 +122,33 @@ def test_synth_fp8_pages_round_like_torch(fmt):
             amax = np.abs(x).reshape(2 * hkv, -1, 32).max(axis=2)
             clean = ok.numpy().reshape(2 * hkv, -1, 32).all(axis=2)
             assert np.array_equal(e[clean], (np.floor(np.log2(amax)) - 8)[clean])
+
+
+def test_tree_entry_points_take_16_token_blocks_only():
+    """Decode pages hold 16 tokens: the tree entry points refuse trees of
+    other block sizes (an 8-token tree's last_page_len would be wrong for a
+    16-token page) with DH_EUNSUPPORTED, before touching any device."""
+    from dendrite_amd.cache import KvCache, KvCacheConfig, TreeState
+    L = _lib.lib()
+    for tpb, want in ((8, _lib.DH_EUNSUPPORTED), (16, _lib.DH_OK)):
+        cache = KvCache(KvCacheConfig(num_layers=1, num_kv_heads=1, head_dim=64, max_blocks=16,
+                                      tokens_per_block=tpb))
+        tree = TreeState(cache, tpb)
+        assert tree.tokens_per_block == tpb
+        leaf = tree.fork(0).node_id
+        for t in range(12):
+            tree.append_token(leaf, t)
+        nodes = np.array([leaf], dtype=np.uint64)
+        lpl = np.zeros(1, dtype=np.int32)
+        rc = L.dh_tree_last_page_len(tree._h, nodes.ctypes.data_as(_lib._PU64), 1,
+                                     lpl.ctypes.data_as(C.POINTER(C.c_int32)))
+        assert rc == want
+        if rc == _lib.DH_OK:
+            assert lpl[0] == 12
+        cfg = AttentionConfig(8, 8, 64).to_c()
+        plan = C.c_void_p()
+        rc = L.dh_plan_create_tree(None, C.byref(cfg), None, tree._h, nodes.ctypes.data_as(_lib._PU64), 1, 1,
+                                   None, C.byref(plan))
+        if tpb != 16:
+            assert rc == _lib.DH_EUNSUPPORTED and b"16" in C.string_at(L.dh_last_error())
+        assert not plan.value

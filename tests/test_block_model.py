@@ -7,16 +7,41 @@ assertion:
   BlockPool   crates/dendrite-core/src/cache/pool.rs:120-272
   KvCache     crates/dendrite-core/src/cache/mod.rs:145-248 (+ proptests :251-365)
   TreeState   crates/dendrite-core/src/tree/state.rs:214-650
-The product under test is the C++ block model in libdendrite_hip.so, reached
-through dendrite_amd.cache (host code only: no GPU is touched).
+Each ported test runs twice: against the product, the C++ block model in
+libdendrite_hip.so reached through dendrite_amd.cache (host code only: no GPU
+is touched), and against the test oracle's pure-Python restatement
+(oracle/block_model.py, through tests/_block_model_oracle_api.py), so the
+reference's own assertions pin both.
 """
 import pytest
-from hypothesis import given, settings, strategies as st
+from hypothesis import HealthCheck, given, settings, strategies as st
 
+import dendrite_amd.cache as _product
 from dendrite_amd import DhError
 from dendrite_amd.cache import (BlockId, BlockPool, BlockTable, KvCache, KvCacheConfig, NodeId,
                                 TreeState)
 from oracle import block_model as ref
+
+import _block_model_oracle_api as _oracle_api
+
+_NAMES = ("BlockId", "BlockPool", "BlockTable", "KvCache", "KvCacheConfig", "NodeId", "TreeState")
+_IMPLS = {
+    "product": dict({n: getattr(_product, n) for n in _NAMES}, DhError=DhError),
+    "oracle": dict({n: getattr(_oracle_api, n) for n in _NAMES}, DhError=_oracle_api.OracleError),
+}
+# The swap below is a plain rebinding of module names, so a fixture shared
+# by every Hypothesis example is harmless.
+_HC = [HealthCheck.function_scoped_fixture]
+
+
+@pytest.fixture(autouse=True, params=sorted(_IMPLS))
+def impl(request):
+    """Binds the block-model names of this module to one implementation."""
+    g = globals()
+    saved = {n: g[n] for n in _IMPLS["product"]}
+    g.update(_IMPLS[request.param])
+    yield request.param
+    g.update(saved)
 
 
 # ---------------------------------------------------------------- BlockTable
@@ -325,7 +350,7 @@ def test_config_accessible():
 _cfg = st.tuples(st.integers(10, 99), st.sampled_from([8, 16, 32]))
 
 
-@settings(max_examples=60, deadline=None)
+@settings(max_examples=60, deadline=None, suppress_health_check=_HC)
 @given(_cfg, st.integers(0, 49))
 def test_invariant_block_count_consistency(cfg, alloc_count):
     c = _cache(*cfg)
@@ -334,7 +359,7 @@ def test_invariant_block_count_consistency(cfg, alloc_count):
     assert c.free_blocks() + c.used_blocks() == c.total_blocks()
 
 
-@settings(max_examples=60, deadline=None)
+@settings(max_examples=60, deadline=None, suppress_health_check=_HC)
 @given(_cfg, st.integers(1, 19))
 def test_invariant_allocate_free_cycle(cfg, cycles):
     c = _cache(*cfg)
@@ -344,7 +369,7 @@ def test_invariant_allocate_free_cycle(cfg, cycles):
     assert c.free_blocks() == initial
 
 
-@settings(max_examples=60, deadline=None)
+@settings(max_examples=60, deadline=None, suppress_health_check=_HC)
 @given(_cfg, st.integers(0, 9))
 def test_invariant_refcount_matches_shares(cfg, shares):
     c = _cache(*cfg)
@@ -359,7 +384,7 @@ def test_invariant_refcount_matches_shares(cfg, shares):
     assert c.free_blocks() == initial
 
 
-@settings(max_examples=30, deadline=None)
+@settings(max_examples=30, deadline=None, suppress_health_check=_HC)
 @given(_cfg)
 def test_invariant_cow_unshared_identity(cfg):
     c = _cache(*cfg)
@@ -367,7 +392,7 @@ def test_invariant_cow_unshared_identity(cfg):
     assert c.copy_on_write(b) == b
 
 
-@settings(max_examples=30, deadline=None)
+@settings(max_examples=30, deadline=None, suppress_health_check=_HC)
 @given(_cfg)
 def test_invariant_cow_shared_creates_new(cfg):
     c = _cache(*cfg)
@@ -585,12 +610,14 @@ _ops = st.lists(st.tuples(st.sampled_from(["fork", "append", "append", "append",
                           st.integers(0, 10 ** 6)), min_size=1, max_size=120)
 
 
-@settings(max_examples=120, deadline=None)
+@settings(max_examples=120, deadline=None, suppress_health_check=_HC)
 @given(_ops, st.integers(4, 64))
-def test_tree_matches_python_restatement(ops, max_blocks):
+def test_tree_matches_python_restatement(impl, ops, max_blocks):
     """Random fork/append/release sequences drive the C++ tree and the Python
     restatement side by side; block tables, CoW pairs, refcounts, free counts
     and error outcomes must agree exactly."""
+    if impl != "product":
+        return          # product against oracle: one run covers it
     cache = _cache(max_blocks)
     tree = TreeState(cache, 16)
     rpool = ref.BlockPool(max_blocks, 16)

@@ -308,3 +308,35 @@ def test_reference_backend_prefill_gqa():
     key, value = torch.randn(1, 2, 4, 64), torch.randn(1, 2, 4, 64)
     output = backend.prefill(query, key, value, BlockTable(16), config)
     assert tuple(output.shape) == tuple(query.shape)
+
+
+@pytest.mark.parametrize("kvf", [_lib.KV_F32, _lib.KV_FP8_E4M3])
+def test_append_kv_leaves_no_unwritten_tokens(kvf):
+    """append_kv writes at offset position % 16, so it must never leave
+    tokens in front of the write unwritten: after clear_cache (which forgets
+    every block but keeps the pool's bytes), an append at position 17 into a
+    block holding nothing is refused; appends from the block's front are
+    accepted, and decode then sees exactly the tokens written."""
+    hkv, d = 2, 64
+    be = HipBackend(num_pages=8, num_kv_heads=hkv, head_dim=d, kv_format=kvf)
+    table = BlockTable.from_blocks([3, 5], num_tokens=18)
+    be.append_kv(_randn((1, hkv, 16, d), 40), _randn((1, hkv, 16, d), 41), table, 0)
+    be.append_kv(_randn((1, hkv, 2, d), 42), _randn((1, hkv, 2, d), 43), table, 16)
+    be.clear_cache()
+    with pytest.raises(DhError) as e:
+        be.append_kv(_randn((1, hkv, 1, d), 44), _randn((1, hkv, 1, d), 45), table, 17)
+    assert e.value.status == _lib.DH_EUNSUPPORTED
+    assert 5 not in be.page_len
+    # refill from the front: token 16 then 17 of block 5 (block 3 stays forgotten)
+    v16, v17 = _randn((1, hkv, 1, d), 47), _randn((1, hkv, 1, d), 49)
+    be.append_kv(_randn((1, hkv, 1, d), 46), v16, table, 16)
+    be.append_kv(_randn((1, hkv, 1, d), 48), v17, table, 17)
+    assert be.page_len[5] == 2 and 3 not in be.page_len
+    if kvf == _lib.KV_F32:
+        cfg = AttentionConfig(hkv, hkv, d)
+        cfg.q_dtype = _lib.DTYPE_F32
+        cfg.kv_format = kvf
+        q = torch.zeros((1, hkv, 1, d))          # zero query: equal weights over the tokens seen
+        out = be.decode(q, table, cfg).cpu().reshape(hkv, d).numpy()
+        want = 0.5 * (v16 + v17).reshape(hkv, d).numpy()
+        assert np.max(np.abs(out - want)) < 1e-6
