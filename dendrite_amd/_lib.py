@@ -32,6 +32,7 @@ PLAN_FLAT, PLAN_CASCADE = 0, 1
 PLAN_APPEND, PLAN_REPLACE_LAST = 0, 1
 
 PAGE_SIZE = 16
+STATIC_WORKSPACE_BYTES = 32 << 20   # DH_STATIC_WORKSPACE_BYTES
 MAX_SEQ_LEN = 131072
 INVALID_PAGE = 0xFFFFFFFF
 INVALID_NODE = 0xFFFFFFFFFFFFFFFF
@@ -119,6 +120,7 @@ SIGNATURES = {
                              _PU32, _PU32, _PU32, _PU32]),
     "dh_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "dh_decode_stages": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _U32, _P]),
+    "dh_decode_batch_static": (_I, [_P, _P, _P, _P, _P, _P, _P]),
     "dh_merge_states": (_I, [_P, _P, _P, _P, _P, _P, _U32, _U32, _P]),
     "dh_gather_debug": (_I, [_P, _PU32, _U32, _U32, _P, _PU32, _P]),
     "dh_debug_e4m3_to_bf16": (_I, [_I, _P, _P, _U32, _P]),

@@ -92,6 +92,9 @@ private:
 struct dh_backend {
     int device;
     std::atomic<int> refs;
+    // Device address of the GPU's static scratch array (dh_decode_batch_static),
+    // looked up once at dh_create with the device current.
+    void* scratch;
 };
 
 static dh_backend* retain(dh_backend* be) {
@@ -222,10 +225,18 @@ dh_status dh_create(int device, dh_backend** out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(DH_EUNSUPPORTED, "device %d is %s; this library is built for gfx950", device,
                     prop.gcnArchName);
+    void* scratch = nullptr;
+    {
+        DH_DEVICE(device);
+        const hipError_t e = hipError_t(dh::static_scratch_address(&scratch));
+        if (e != hipSuccess || !scratch)
+            return fail(DH_EHIP, "static scratch of device %d: %s", device, hipGetErrorString(e));
+    }
     dh_backend* be = new (std::nothrow) dh_backend;
     if (!be) return fail(DH_ENOMEM, "out of host memory");
     be->device = device;
     be->refs.store(1, std::memory_order_relaxed);
+    be->scratch = scratch;
     *out = be;
     return DH_OK;
 }
@@ -817,9 +828,11 @@ static dh_status check_device_ptr(const void* p, const char* what) {
     return DH_OK;
 }
 
+// ws_static: ws is the backend's static scratch (device memory by
+// construction; the runtime does not track module globals as allocations).
 static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
                              const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes, uint32_t mask,
-                             void* stream) {
+                             void* stream, bool ws_static) {
     if (!be || !pool || !pl) return fail(DH_EINVAL, "NULL argument");
     if (pl->be != be || pool->be != be) return fail(DH_EINVAL, "plan/pool belong to another backend");
     if (pool->num_pages != pl->pool_pages || pool->hkv != pl->cfg.num_kv_heads ||
@@ -835,7 +848,7 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
     if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
     DH_DEVICE(be->device);
     for (const auto& [ptr, what] : {std::pair<const void*, const char*>{q, "q"}, {out, "out"},
-                                    {pl->ws_bytes ? ws : nullptr, "workspace"},
+                                    {pl->ws_bytes && !ws_static ? ws : nullptr, "workspace"},
                                     {last_page_len, "last_page_len"}}) {
         if (!ptr) continue;
         const dh_status st = check_device_ptr(ptr, what);
@@ -893,13 +906,23 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
 dh_status dh_decode_stages(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
                            const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
                            uint32_t mask, void* stream) {
-    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, mask, stream);
+    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, mask, stream, false);
 }
 
 dh_status dh_decode_batch(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
                           void* stream) {
-    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream);
+    return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream, false);
+}
+
+dh_status dh_decode_batch_static(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                                 const int32_t* last_page_len, void* out, void* stream) {
+    if (!be || !pl) return fail(DH_EINVAL, "NULL argument");
+    if (pl->ws_bytes > DH_STATIC_WORKSPACE_BYTES)
+        return fail(DH_ENOMEM, "the plan needs %zu bytes of partial states; the static scratch holds %zu "
+                    "(use dh_decode_batch with a workspace)", pl->ws_bytes, size_t(DH_STATIC_WORKSPACE_BYTES));
+    return decode_impl(be, pool, pl, q, last_page_len, out, be->scratch, DH_STATIC_WORKSPACE_BYTES, 3u, stream,
+                       true);
 }
 
 /* ------------------------------------------------------------------- merge */

@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include "dh_device.hpp"
+#include "dendrite_hip.h"
 
 namespace dh {
 namespace {
@@ -2291,7 +2292,16 @@ hipError_t launch_merge_d(const MergeArgs& a, uint32_t q_dtype, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Partial-state memory of dh_decode_batch_static: DH_STATIC_WORKSPACE_BYTES
+// per GPU, held from the library's load to the end of the process.  Host
+// code never uses this name as an address (on the host it is a stand-in,
+// not device memory); it asks for the array's device address once per GPU
+// (static_scratch_address, from dh_create) and passes that pointer.
+static __device__ __align__(256) uint8_t scratch[DH_STATIC_WORKSPACE_BYTES];
+
 }  // namespace
+
+int static_scratch_address(void** out) { return int(hipGetSymbolAddress(out, HIP_SYMBOL(scratch))); }
 
 bool attend_supported(uint32_t q_dtype, uint32_t kvf, uint32_t d) {
     if (d != 64 && d != 128 && d != 256) return false;

@@ -145,6 +145,9 @@ int launch_plan_patch(uint32_t* words, uint32_t n, const uint32_t* idx, const ui
 int launch_write_pages(const uint32_t* ids, uint32_t n, const void* src, uint32_t src_dtype, uint8_t* data,
                        uint8_t* scales, uint32_t num_pages, uint32_t hkv, uint32_t d, uint32_t fmt,
                        void* stream);
+// Device address of this GPU's static scratch array (decode_kernels.hip);
+// call with the GPU current.  Returns hipError_t as int.
+int static_scratch_address(void** out);
 int launch_attend(const AttendArgs& a, uint32_t n_tasks, uint32_t q_dtype, uint32_t kv_format,
                   uint32_t head_dim, bool prefill, void* stream);
 int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t head_dim, void* stream);

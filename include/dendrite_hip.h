@@ -355,6 +355,24 @@ dh_status dh_decode_batch(dh_backend* backend, const dh_pool* pool,
                           const int32_t* last_page_len, void* out,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static scratch array behind dh_decode_batch_static (per GPU). */
+#define DH_STATIC_WORKSPACE_BYTES (32u << 20)
+
+/* dh_decode_batch that allocates nothing and takes no workspace: the partial
+ * states go to a static device array of DH_STATIC_WORKSPACE_BYTES that the
+ * library holds on every GPU it runs on until the process ends (its address
+ * is looked up once per GPU by dh_create).  No counterpart in the reference:
+ * for callers that cannot allocate device memory at decode time (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Plans whose dh_plan_workspace_size exceeds DH_STATIC_WORKSPACE_BYTES are
+ * refused with DH_ENOMEM.  Every call on one GPU uses the same array, so
+ * calls that overlap on one GPU (different streams or threads) race: order
+ * them on one stream.  Nothing in the array needs clearing between calls
+ * (every partial state a decode reads, it wrote).  Arguments and results as
+ * dh_decode_batch. */
+dh_status dh_decode_batch_static(dh_backend* backend, const dh_pool* pool, const dh_plan* plan,
+                                 const void* q, const int32_t* last_page_len, void* out, void* stream);
+
 /* Stages of dh_decode_batch, for profiling: bit 0 = attention items,
  * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3.  A prefill
  * plan in which every query row is one work item's (one partial state per
