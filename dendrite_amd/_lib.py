@@ -1,7 +1,8 @@
 """ctypes binding of libdendrite_hip.so (the C ABI in include/dendrite_hip.h).
 
-The library is loaded from the package directory only; a missing library is a
-hard error (there is no fallback implementation).
+The library is loaded from the package directory (or from the path in
+DENDRITE_HIP_LIB, e.g. the host-sanitized build); a missing library is a hard
+error (there is no fallback implementation).
 """
 from __future__ import annotations
 
@@ -9,7 +10,7 @@ import ctypes as C
 import os
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG, "libdendrite_hip.so")
+LIB_PATH = os.environ.get("DENDRITE_HIP_LIB") or os.path.join(_PKG, "libdendrite_hip.so")
 
 # dh_status
 DH_OK = 0

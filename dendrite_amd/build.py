@@ -2,6 +2,13 @@
 
 Usage: python -m dendrite_amd.build  (or dendrite_amd.build.build()).
 Every call compiles from scratch; objects go to dendrite_amd/_build/.
+
+python -m dendrite_amd.build --sanitize builds a second library,
+dendrite_amd/_build_san/libdendrite_hip.so, whose host code (api, planner,
+block model, synth) carries AddressSanitizer and UndefinedBehaviorSanitizer
+(the kernels are built as usual).  Load it in place of the product library
+with the sanitizer runtime preloaded; the command it prints runs the CPU test
+suite that way.
 """
 from __future__ import annotations
 
@@ -29,6 +36,13 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-fno-honor-nans", "-mno-amdgpu-ieee"]
 HOST = ["-D__HIP_PLATFORM_AMD__", f"-I{os.path.join(ROCM, 'include')}", "-x", "c++"]
 
+# Host-only instrumentation: every -fsanitize= on a hipcc line sits behind
+# -Xarch_host, so no device code is built with it.
+SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g", "-O1"]
+SAN_BUILD = os.path.join(PKG, "_build_san")
+SAN_LIB = os.path.join(SAN_BUILD, "libdendrite_hip.so")
+
 HIP_SOURCES = ["decode_kernels.hip", "write_kernels.hip"]
 HOST_SOURCES = ["api.cpp", "planner.cpp", "block_model.cpp", "synth.cpp"]
 
@@ -41,30 +55,53 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{msg}")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link the shared library; returns its path."""
+def build(verbose: bool = False, sanitize: bool = False) -> str:
+    """Compile every source and link the shared library; returns its path.
+    sanitize: the host-sanitized library under _build_san/ instead."""
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    shutil.rmtree(BUILD, ignore_errors=True)
-    os.makedirs(BUILD, exist_ok=True)
+    bdir, lib = (SAN_BUILD, SAN_LIB) if sanitize else (BUILD, LIB)
+    shutil.rmtree(bdir, ignore_errors=True)
+    os.makedirs(bdir, exist_ok=True)
+    host_flags = [*HOST, *SANITIZE] if sanitize else HOST
     jobs = []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD, src + ".o")
+        obj = os.path.join(bdir, src + ".o")
         jobs.append(([HIPCC, *COMMON, *DEVICE, "-c", os.path.join(CSRC, src), "-o", obj], obj))
     for src in HOST_SOURCES:
-        obj = os.path.join(BUILD, src + ".o")
-        jobs.append(([HIPCC, *COMMON, *HOST, "-c", os.path.join(CSRC, src), "-o", obj], obj))
+        obj = os.path.join(bdir, src + ".o")
+        jobs.append(([HIPCC, *COMMON, *host_flags, "-c", os.path.join(CSRC, src), "-o", obj], obj))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for fut in [ex.submit(_run, cmd) for cmd, _ in jobs]:
             fut.result()
-    tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", tmp, *[o for _, o in jobs], "-lpthread"])
-    os.replace(tmp, LIB)
+    tmp = lib + ".tmp"
+    link_san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                "-shared-libsan"] if sanitize else []
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *link_san, "-o", tmp, *[o for _, o in jobs],
+          "-lpthread"])
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
+
+
+def sanitizer_runtime() -> str:
+    """The clang AddressSanitizer runtime the sanitized library links."""
+    proc = subprocess.run([os.path.join(ROCM, "llvm", "bin", "clang"), "-print-file-name=",
+                           "--rtlib=compiler-rt"], capture_output=True, text=True)
+    base = os.path.join(proc.stdout.strip(), "lib", "linux") if proc.returncode == 0 else ""
+    path = os.path.join(base, "libclang_rt.asan-x86_64.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"AddressSanitizer runtime not found at {path!r}")
+    return path
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--sanitize" in sys.argv[1:]:
+        build(verbose=True, sanitize=True)
+        print("run the CPU tests on it with:\n"
+              f"  LD_PRELOAD={sanitizer_runtime()} DENDRITE_HIP_LIB={SAN_LIB} "
+              "ASAN_OPTIONS=detect_leaks=0 python -m pytest tests -m 'not gpu' -q")
+    else:
+        build(verbose=True)
     sys.exit(0)

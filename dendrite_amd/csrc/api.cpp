@@ -689,8 +689,9 @@ dh_status dh_plan_create_prefill(dh_backend* be, const dh_attn_config* cfg, cons
     st = check_pool_matches(cfg, pool);
     if (st != DH_OK) return st;
     const bool fp8 = cfg->kv_format == DH_KV_FP8_E4M3 || cfg->kv_format == DH_KV_MXFP8;
-    if (cfg->q_dtype == DH_DTYPE_F32 || (fp8 && cfg->head_dim == 64))
-        return fail(DH_EUNSUPPORTED, "prefill takes bf16 / f16 queries, and FP8 / MXFP8 KV at head_dim 128 or 256");
+    if (cfg->q_dtype == DH_DTYPE_F32 || (fp8 && (cfg->head_dim == 64 || cfg->q_dtype != DH_DTYPE_BF16)))
+        return fail(DH_EUNSUPPORTED, "prefill takes bf16 / f16 queries over 16-bit KV, and bf16 queries over "
+                    "FP8 / MXFP8 KV at head_dim 128 or 256");
     if (batch && (!indptr || !kv_len || !q_len)) return fail(DH_EINVAL, "NULL argument");
     if (batch && indptr[batch] > indptr[0] && !indices) return fail(DH_EINVAL, "indices is NULL");
     dh::PrefillInput in;

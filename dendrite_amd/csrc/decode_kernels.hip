@@ -107,6 +107,20 @@ __device__ __forceinline__ void e4m3x4_to_bf16(uint32_t x, float sc, uint32_t& l
     hi = __builtin_bit_cast(uint32_t, b);
 }
 
+// The same into f16 (H) or bf16: 8-bit pools under f16 queries compute in
+// f16 (every E4M3 code is exact in f16; code x scale rounds once).
+template <bool H>
+__device__ __forceinline__ void e4m3x4_cvt(uint32_t x, float sc, uint32_t& lo, uint32_t& hi) {
+    if constexpr (H) {
+        f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, sc, false);
+        f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, sc, true);
+        lo = __builtin_bit_cast(uint32_t, a);
+        hi = __builtin_bit_cast(uint32_t, b);
+    } else {
+        e4m3x4_to_bf16(x, sc, lo, hi);
+    }
+}
+
 __device__ __forceinline__ uint32_t pack2(float a, float b, bool f16) {
     if (f16) {
         f16x2 t = {(_Float16)a, (_Float16)b};
@@ -457,8 +471,9 @@ __device__ __forceinline__ void load_page_v(PageRaw<D, KVF>& r, const AttendArgs
     }
 }
 
-// K rows of a page as MFMA A operands (bf16/f16 dwords).
-template <int D, uint32_t KVF>
+// K rows of a page as MFMA A operands (bf16/f16 dwords; 8-bit codes into
+// f16 when H).
+template <int D, uint32_t KVF, bool H>
 __device__ __forceinline__ void k_operand(const PageRaw<D, KVF>& r, uint32_t (&op)[D / 32][4]) {
     using R = PageRaw<D, KVF>;
     #pragma unroll
@@ -468,8 +483,8 @@ __device__ __forceinline__ void k_operand(const PageRaw<D, KVF>& r, uint32_t (&o
             for (int w = 0; w < 4; ++w) op[kb][w] = r.k[kb][w];
         } else {
             const float sc = KVF == KVF_MX ? e8m0_to_float(r.ksc[kb]) : 1.f;
-            e4m3x4_to_bf16(r.k[kb][0], sc, op[kb][0], op[kb][1]);
-            e4m3x4_to_bf16(r.k[kb][1], sc, op[kb][2], op[kb][3]);
+            e4m3x4_cvt<H>(r.k[kb][0], sc, op[kb][0], op[kb][1]);
+            e4m3x4_cvt<H>(r.k[kb][1], sc, op[kb][2], op[kb][3]);
         }
     }
 }
@@ -477,7 +492,7 @@ __device__ __forceinline__ void k_operand(const PageRaw<D, KVF>& r, uint32_t (&o
 // V rows of a page (tokens 4g+j, dims c*EPL..) as bf16/f16 dwords; rows of
 // tokens at or beyond nt are zero so that garbage past the valid tokens can
 // never reach the accumulator (their probabilities are zero).
-template <int D, uint32_t KVF>
+template <int D, uint32_t KVF, bool H>
 __device__ __forceinline__ void v_operand(const PageRaw<D, KVF>& r, int g, int nt,
                                           uint32_t (&op)[4][D / 32]) {
     using R = PageRaw<D, KVF>;
@@ -491,7 +506,7 @@ __device__ __forceinline__ void v_operand(const PageRaw<D, KVF>& r, int g, int n
             const float sc = KVF == KVF_MX ? e8m0_to_float(r.vsc[j]) : 1.f;
             #pragma unroll
             for (int w = 0; w < R::VW; ++w)
-                e4m3x4_to_bf16(ok ? r.v[j][w] : 0u, sc, op[j][2 * w], op[j][2 * w + 1]);
+                e4m3x4_cvt<H>(ok ? r.v[j][w] : 0u, sc, op[j][2 * w], op[j][2 * w + 1]);
         }
     }
 }
@@ -576,8 +591,8 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
         const int n0 = page_tokens(it, i0, last_len);
         const int n1 = page_tokens(it, i0 + 1, last_len);
         uint32_t kop[2][KB][4];
-        k_operand<D, KVF>(pr[buf][0], kop[0]);
-        k_operand<D, KVF>(pr[buf][1], kop[1]);
+        k_operand<D, KVF, F16>(pr[buf][0], kop[0]);
+        k_operand<D, KVF, F16>(pr[buf][1], kop[1]);
         f4 sc[1][2];
         pair_scores<D, F16, 1, 1>(kop, qB, sc);
         const float f0 = a.scale_log2 * ks[buf][0], f1 = a.scale_log2 * ks[buf][1];
@@ -587,11 +602,11 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
         uint32_t vop[2][4][D / 32];
         const bool full = (n0 == kPageSize) && (n1 == kPageSize);
         if (full) {
-            v_operand<D, KVF>(pr[buf][0], g, kPageSize, vop[0]);
-            v_operand<D, KVF>(pr[buf][1], g, kPageSize, vop[1]);
+            v_operand<D, KVF, F16>(pr[buf][0], g, kPageSize, vop[0]);
+            v_operand<D, KVF, F16>(pr[buf][1], g, kPageSize, vop[1]);
         } else {
-            v_operand<D, KVF>(pr[buf][0], g, n0, vop[0]);
-            v_operand<D, KVF>(pr[buf][1], g, n1, vop[1]);
+            v_operand<D, KVF, F16>(pr[buf][0], g, n0, vop[0]);
+            v_operand<D, KVF, F16>(pr[buf][1], g, n1, vop[1]);
         }
         pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(sc, vop, n0, n1, f0, f1, v0s, v1s, m, L, O, g);
         if (refill) load_pair(buf, pi + DEPTH, false);
@@ -675,8 +690,9 @@ __device__ __forceinline__ void group_commit(uint8_t* stage, const Staged<D, KVF
     }
 }
 
-// Reads one wave's K / V operands of a staged pair from LDS.
-template <int D, uint32_t KVF>
+// Reads one wave's K / V operands of a staged pair from LDS (8-bit codes
+// into f16 when H, else bf16).
+template <int D, uint32_t KVF, bool H>
 __device__ __forceinline__ void group_operands(const uint8_t* stage, int g, int c, int n0, int n1,
                                                uint32_t (&kop)[2][D / 32][4],
                                                uint32_t (&vop)[2][4][D / 32]) {
@@ -694,8 +710,8 @@ __device__ __forceinline__ void group_operands(const uint8_t* stage, int g, int 
                 load_dwords<2>(raw, kp + kb * 32 + 8 * g);
                 float sc = 1.f;
                 if constexpr (KVF == KVF_MX) sc = e8m0_to_float(stage[4 * L::PLANE + p * L::SREC + c * L::G + kb]);
-                e4m3x4_to_bf16(raw[0], sc, kop[p][kb][0], kop[p][kb][1]);
-                e4m3x4_to_bf16(raw[1], sc, kop[p][kb][2], kop[p][kb][3]);
+                e4m3x4_cvt<H>(raw[0], sc, kop[p][kb][0], kop[p][kb][1]);
+                e4m3x4_cvt<H>(raw[1], sc, kop[p][kb][2], kop[p][kb][3]);
             }
         }
     }
@@ -720,7 +736,7 @@ __device__ __forceinline__ void group_operands(const uint8_t* stage, int g, int 
                     sc = e8m0_to_float(stage[4 * L::PLANE + (2 + p) * L::SREC + tok * L::G + (c * EPL) / 32]);
                 #pragma unroll
                 for (int w = 0; w < EPL / 4; ++w)
-                    e4m3x4_to_bf16(ok ? raw[w] : 0u, sc, vop[p][j][2 * w], vop[p][j][2 * w + 1]);
+                    e4m3x4_cvt<H>(ok ? raw[w] : 0u, sc, vop[p][j][2 * w], vop[p][j][2 * w + 1]);
             }
         }
     }
@@ -758,7 +774,7 @@ __device__ __forceinline__ void group_loop(const AttendArgs& a, const Item& it, 
             }
             uint32_t kop[2][D / 32][4];
             uint32_t vop[2][4][D / 32];
-            group_operands<D, KVF>(stage, g, c, n0, n1, kop, vop);
+            group_operands<D, KVF, F16>(stage, g, c, n0, n1, kop, vop);
             f4 s[RT][2];
             pair_scores<D, F16, NRT, RT>(kop, qB, s);
             pair_softmax_pv<D, F16, NRT, RT, BLOCK_SCALE>(s, vop, n0, n1, f0, f1, v0s, v1s, m, Lsum, O, g);
@@ -1006,14 +1022,15 @@ __device__ __forceinline__ void mask_v_tr(u32x4& v, int w0, int g, int n) {
 
 // Softmax pieces of the DMA path.  Scores are in log2 units once multiplied
 // by f = scale_log2 > 0 (a negative scale is folded into the query's sign).
-// A row's reference max m moves only when a score passes it by kLazyDma;
-// in between, exp2(x - m) stays below 2^kLazyDma, far inside f32 / bf16 /
-// f16-after-row-sum range, so the accumulators are not rescaled on the
-// common path.  The check compares the lane's raw score max with
+// A row's reference max m moves only when a score passes it by kLazyDma
+// (kLazyDma16 when the probabilities are packed as f16); in between,
+// exp2(x - m) stays below 2^32 (bf16 range) or 2^14 (f16, whose range ends
+// at 2^16), so the accumulators are not rescaled on the common path.  The check compares the lane's raw score max with
 // thr = (m + kLazyDma) / f, kept per row, so the common path spends no
 // multiply on it.  The move (always on the item's first pair, where m and
 // thr start at -inf) runs on a slow path.
 constexpr float kLazyDma = 32.f;
+constexpr float kLazyDma16 = 14.f;
 
 template <int RT>
 struct RowMax {
@@ -1061,7 +1078,7 @@ __device__ __forceinline__ float dma_lane_max_ks(f4 (&s)[RT][2], int rt, int n0,
 
 // The slow path: moves m of every row whose scores passed thr and rescales
 // its accumulators.  Rows that did not move get alpha = 1.
-template <int D, int NRT>
+template <int D, int NRT, bool F16>
 __device__ __forceinline__ void dma_rescale(const float (&lm)[DmaCfg<D>::RT], RowMax<DmaCfg<D>::RT>& rm,
                                          f4 (&Lsum)[DmaCfg<D>::RT], f4 (&O)[DmaCfg<D>::RT][D / 16], float f,
                                          float finv) {
@@ -1072,7 +1089,7 @@ __device__ __forceinline__ void dma_rescale(const float (&lm)[DmaCfg<D>::RT], Ro
             const float mnew = mx * f;
             const float alpha = rm.m[rt] == kNegInf ? 0.f : fast_exp2(rm.m[rt] - mnew);
             rm.m[rt] = mnew;
-            rm.thr[rt] = (mnew + kLazyDma) * finv;
+            rm.thr[rt] = (mnew + (F16 ? kLazyDma16 : kLazyDma)) * finv;
             Lsum[rt] *= alpha;
             #pragma unroll
             for (int e = 0; e < D / 16; ++e) O[rt][e] *= alpha;
@@ -1267,7 +1284,7 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
         else lm[rt] = dma_lane_max<RT, PART>(sc, rt, pm.s0[rt], pm.s1[rt], g);
         need |= lm[rt] > rm.thr[rt];
     }
-    if (__ballot(need)) dma_rescale<D, NRT>(lm, rm, Lsum, O, f, finv);
+    if (__ballot(need)) dma_rescale<D, NRT, F16>(lm, rm, Lsum, O, f, finv);
     // Branch-free from here, so the scheduler sees one region: LDS reads
     // first, then the score MFMAs of pair p + 1 interleaved with the
     // softmax of pair p (a wave overlaps some of its VALU work with MFMAs
@@ -1708,7 +1725,7 @@ __device__ __forceinline__ void dma8_pair(const AttendArgs& a, const Item& it, u
 }
 
 // Converts raw slot rs into bf16 slot bs (the whole workgroup; tid < 256).
-template <int D, uint32_t KVF>
+template <int D, uint32_t KVF, bool H>
 __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_t bs, int tid) {
     using C8 = Dma8Cfg<D>;
     using C = DmaCfg<D>;
@@ -1728,14 +1745,14 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
         if constexpr (KVF == KVF_MX) {
             const float sc = e8m0_to_float(scl[(page * 2 + plane) * C8::SREC + row * (D / 32) + col0 / 32]);
             #pragma unroll
-            for (int w = 0; w < 8; ++w) e4m3x4_to_bf16(wd[w], sc, out[2 * w], out[2 * w + 1]);
+            for (int w = 0; w < 8; ++w) e4m3x4_cvt<H>(wd[w], sc, out[2 * w], out[2 * w + 1]);
         } else if (plane == 0) {
             // K: the codes alone (exact in bf16); the block scale multiplies
             // the scores, so the attention scale does not amplify a rounding
             // of code * scale.  (plane is wave-uniform: a wave converts 2048
             // consecutive bytes, whole planes at head_dim 128 and 256.)
             #pragma unroll
-            for (int w = 0; w < 8; ++w) e4m3x4_to_bf16(wd[w], 1.f, out[2 * w], out[2 * w + 1]);
+            for (int w = 0; w < 8; ++w) e4m3x4_cvt<H>(wd[w], 1.f, out[2 * w], out[2 * w + 1]);
         } else {
             // V: code * scale in f32, rounded once to bf16 (RNE).
             const float sc = *reinterpret_cast<const float*>(scl + 4 * (page * 2 + plane));
@@ -1743,8 +1760,8 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
             for (int w = 0; w < 8; ++w) {
                 const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], false);
                 const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], true);
-                out[2 * w] = pack2(lo[0] * sc, lo[1] * sc, false);
-                out[2 * w + 1] = pack2(hi[0] * sc, hi[1] * sc, false);
+                out[2 * w] = pack2(lo[0] * sc, lo[1] * sc, H);
+                out[2 * w + 1] = pack2(hi[0] * sc, hi[1] * sc, H);
             }
         }
         uint8_t* rowp = bf + page * C::PAGE + plane * C::PLANE + row * C::RB;
@@ -1756,7 +1773,7 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
     }
 }
 
-template <int D, uint32_t KVF, int NRT, bool TAIL, bool CAUSAL>
+template <int D, uint32_t KVF, bool F16, int NRT, bool TAIL, bool CAUSAL>
 __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                 uint8_t* ring, int tid, int wave, int g, int c,
                                                 const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
@@ -1817,11 +1834,11 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
     }
     wait_vmcnt_any((pro - 1) * C8::PER_PAIR);   // raw pair 0 has landed
     block_barrier();                             // query rows read; raw pair 0 visible
-    dma8_convert<D, KVF>(ring, 0, 0, tid);
+    dma8_convert<D, KVF, F16>(ring, 0, 0, tid);
     block_barrier();
     f4 sc[RT][2];
     u32x4 vop[D / 16];
-    if constexpr (NRT > 0) dma_scores<D, false, NRT>(0, lb, qB, sc);
+    if constexpr (NRT > 0) dma_scores<D, F16, NRT>(0, lb, qB, sc);
     uint32_t ps = 0, psn = 1;   // raw slots of pairs pi, pi + 1
     uint32_t nid0 = page_id(2 * (P - 1)), nid1 = page_id(2 * (P - 1) + 1);
     // Step pi: raw pair pi + 1 is converted into bf16 slot (pi + 1) & 1 while
@@ -1840,18 +1857,18 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
             if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
             nid0 = page_id(2 * (pi + P));
             nid1 = page_id(2 * (pi + P) + 1);
-            dma8_convert<D, KVF>(ring, psn, (j + 1) & 1, tid);
+            dma8_convert<D, KVF, F16>(ring, psn, (j + 1) & 1, tid);
             block_barrier();
             if constexpr (NRT > 0) {
                 float ks0 = 1.f, ks1 = 1.f;
                 if constexpr (KS) k_scales(ps, ks0, ks1);
                 const int t = CAUSAL ? int(lim.tok0 + 2 * kPageSize * pi) : 0;
                 if (CAUSAL && t + 2 * kPageSize > int(lim.lmin))
-                    dma_step<D, false, NRT, true, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                    dma_step<D, F16, NRT, true, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
                                                             causal_mask<RT>(t, rtg.len, int(lim.lmax)), lb, qB, sc,
                                                             vop, rm, Lsum, O, g, f, finv, ks0, ks1);
                 else
-                    dma_step<D, false, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                    dma_step<D, F16, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
                                                              uniform_mask<RT>(kPageSize, kPageSize), lb, qB, sc,
                                                              vop, rm, Lsum, O, g, f, finv, ks0, ks1);
             }
@@ -1873,12 +1890,12 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
         }
         float ks0 = 1.f, ks1 = 1.f;
         if constexpr (KS) k_scales(ps, ks0, ks1);
-        dma_step<D, false, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, pm, lb, qB, sc, vop, rm, Lsum, O, g,
+        dma_step<D, F16, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, pm, lb, qB, sc, vop, rm, Lsum, O, g,
                                                 f, finv, ks0, ks1);
     }
 }
 
-template <int D, uint32_t KVF, int NRT, bool PF>
+template <int D, uint32_t KVF, bool F16, int NRT, bool PF>
 __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                uint8_t* ring, int tid, int wave, int g, int c,
                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
@@ -1898,19 +1915,19 @@ __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& 
     }
     if constexpr (PF) {   // prefill plans: every item is causal
         const ItemLim lim = a.item_lim[blockIdx.x];
-        dma8_group_loop<D, KVF, NRT, false, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm,
+        dma8_group_loop<D, KVF, F16, NRT, false, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm,
                                                   L, O);
     } else if (it.flags & kItemTail) {
-        dma8_group_loop<D, KVF, NRT, true, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+        dma8_group_loop<D, KVF, F16, NRT, true, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                   qB, rm, L, O);
     } else {
-        dma8_group_loop<D, KVF, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+        dma8_group_loop<D, KVF, F16, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                    qB, rm, L, O);
     }
-    write_partial_dma<D, RT, PF>(a, it, wave, NRT, rtg, rm.m, L, O, g, c, false);
+    write_partial_dma<D, RT, PF>(a, it, wave, NRT, rtg, rm.m, L, O, g, c, F16);
 }
 
-template <int D, uint32_t KVF, bool PF>
+template <int D, uint32_t KVF, bool F16, bool PF>
 __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item& item, int tid, int wave, int g,
                                                 int c) {
     using C = DmaCfg<D>;
@@ -1925,9 +1942,9 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
     __syncthreads();
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
-    if (nrt >= 2) dma8_group_run<D, KVF, C::RT, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else if (nrt == 1) dma8_group_run<D, KVF, 1, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else dma8_group_run<D, KVF, 0, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    if (nrt >= 2) dma8_group_run<D, KVF, F16, C::RT, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else if (nrt == 1) dma8_group_run<D, KVF, F16, 1, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    else dma8_group_run<D, KVF, F16, 0, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
 }
 
 // ---------------------------------------------------------------- attend16
@@ -1941,7 +1958,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     if (blockIdx.x < a.n_group_items) {
         const Item it = a.items[blockIdx.x];
         if constexpr ((KVF == KVF_FP8 || KVF == KVF_MX) && D == 64) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
-        else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, false>(a, it, tid, wave, g, c);
+        else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, F16, false>(a, it, tid, wave, g, c);
         else group_item_dma<D, F16, false>(a, it, tid, wave, g, c);
     } else {
         const uint32_t idx = wave_item_index(a, wave);
@@ -1959,7 +1976,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill16_kernel(Attend
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (blockIdx.x >= a.n_group_items) return;
     const Item it = a.items[blockIdx.x];
-    if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, true>(a, it, tid, wave, g, c);
+    if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, F16, true>(a, it, tid, wave, g, c);
     else group_item_dma<D, F16, true>(a, it, tid, wave, g, c);
 }
 
@@ -2273,6 +2290,10 @@ hipError_t launch_attend_d(const AttendArgs& a, uint32_t n, uint32_t q_dtype, ui
         hipLaunchKernelGGL((attend16_kernel<D, KVF_FP8, false>), grid, block, 0, s, a);
     } else if (q_dtype == 1 && kvf == KVF_MX) {
         hipLaunchKernelGGL((attend16_kernel<D, KVF_MX, false>), grid, block, 0, s, a);
+    } else if (q_dtype == 0 && kvf == KVF_FP8) {   // f16 queries: codes into f16, f16 MFMAs
+        hipLaunchKernelGGL((attend16_kernel<D, KVF_FP8, true>), grid, block, 0, s, a);
+    } else if (q_dtype == 0 && kvf == KVF_MX) {
+        hipLaunchKernelGGL((attend16_kernel<D, KVF_MX, true>), grid, block, 0, s, a);
     } else if (q_dtype == 0 && kvf == KVF_F16) {
         hipLaunchKernelGGL((attend16_kernel<D, KVF_F16, true>), grid, block, 0, s, a);
     } else {
@@ -2306,7 +2327,7 @@ int static_scratch_address(void** out) { return int(hipGetSymbolAddress(out, HIP
 bool attend_supported(uint32_t q_dtype, uint32_t kvf, uint32_t d) {
     if (d != 64 && d != 128 && d != 256) return false;
     return (q_dtype == 2 && kvf == KVF_F32) || (q_dtype == 1 && kvf == KVF_BF16) ||
-           (q_dtype == 1 && kvf == KVF_FP8) || (q_dtype == 1 && kvf == KVF_MX) ||
+           (q_dtype <= 1 && kvf == KVF_FP8) || (q_dtype <= 1 && kvf == KVF_MX) ||
            (q_dtype == 0 && kvf == KVF_F16);
 }
 

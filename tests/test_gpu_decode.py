@@ -78,10 +78,13 @@ SHAPES = [(32, 4, 64), (32, 8, 128), (16, 2, 256), (8, 8, 128), (64, 8, 128)]
 FORMATS = [(_lib.DTYPE_BF16, _lib.KV_BF16), (_lib.DTYPE_F16, _lib.KV_F16),
            (_lib.DTYPE_F32, _lib.KV_F32), (_lib.DTYPE_BF16, _lib.KV_FP8_E4M3),
            (_lib.DTYPE_BF16, _lib.KV_MXFP8)]
+# f16 queries over 8-bit pools (BatchDecodeConfig.dtype 0 = f16 with any cache).
+FORMATS_F16Q = [(_lib.DTYPE_F16, _lib.KV_FP8_E4M3), (_lib.DTYPE_F16, _lib.KV_MXFP8)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-@pytest.mark.parametrize("fmt", FORMATS, ids=["bf16", "f16", "f32", "fp8", "mxfp8"])
+@pytest.mark.parametrize("fmt", FORMATS + FORMATS_F16Q,
+                         ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8", "f16q-mxfp8"])
 def test_random_trees(backend, shape, fmt):
     """Random fork trees with partial last pages, every head shape and format,
     cascade and flat plans."""
@@ -93,7 +96,8 @@ def test_random_trees(backend, shape, fmt):
 
 @pytest.mark.parametrize("scale", [-0.25, 0.0, 1.5], ids=["negative", "zero", "large"])
 @pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256)], ids=lambda s: "x".join(map(str, s)))
-@pytest.mark.parametrize("fmt", [FORMATS[0], FORMATS[1], FORMATS[3], FORMATS[4]], ids=["bf16", "f16", "fp8", "mxfp8"])
+@pytest.mark.parametrize("fmt", [FORMATS[0], FORMATS[1], FORMATS[3], FORMATS[4]] + FORMATS_F16Q,
+                         ids=["bf16", "f16", "fp8", "mxfp8", "f16q-fp8", "f16q-mxfp8"])
 def test_scales(backend, shape, fmt, scale):
     """Scales other than 1/sqrt(D): a negative scale (folded into the query's
     sign on the shared-prefix path), zero (uniform weights) and a large one
@@ -102,6 +106,40 @@ def test_scales(backend, shape, fmt, scale):
     w = workloads.random_tree(21, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
     _check(w, backend, scale=scale)
 
+
+
+@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("fmt", [FORMATS[0], FORMATS[1]], ids=["bf16", "f16"])
+def test_scores_rising_late(backend, shape, fmt):
+    """Scores that climb far above the first pages' inside one item (keys of
+    the prefix's second half scaled by 8, scale 1.5: a spread of ~100 log2
+    units).  The lazily moved running max must keep every probability inside
+    the range of the type it is packed in for the PV product (2^16 for f16):
+    a slack of 32 log2 units overflowed f16 to inf and the output to NaN."""
+    hq, hkv, d = shape
+    prefix = list(range(10, 26))
+    tables = [prefix + [40 + i] for i in range(6)]
+    w = workloads.custom(tables, hq, hkv, d, fmt[0], fmt[1], 64, last_page_len=[9] * 6,
+                         name="rising")
+    run = GpuRun(w, backend, scale=1.5)
+    dt = np.float16 if fmt[1] == _lib.KV_F16 else None
+    x = run.data.view(np.uint16).reshape(len(run.ids), 2, hkv, 16, d)
+    late = np.isin(run.ids, prefix[8:])
+    if dt is not None:
+        k = x[late, 0].view(np.float16).astype(np.float32) * 8.0
+        x[late, 0] = k.astype(np.float16).view(np.uint16)
+    else:   # bf16: scale by 8 = add 3 to the exponent (no value here is near overflow)
+        k = (x[late, 0].astype(np.uint32) << 16).view(np.float32) * 8.0
+        x[late, 0] = (k.view(np.uint32) >> 16).astype(np.uint16)
+    run.pool.write_pages(run.ids, run.data, run.scales)
+    got = run.run()
+    ref = run.reference()
+    raw = max_abs_err(got, ref)
+    err = excess_err(got, ref, w.q_dtype)
+    print(f"[case] rising {shape} fmt={fmt}: max abs err {raw:.3e}, beyond output rounding {err:.3e}",
+          flush=True)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    assert err <= TOL[w.q_dtype], err
 
 def test_empty_sequences(backend):
     """Sequences without pages get zeros (backend.rs:218-222), also when no

@@ -94,6 +94,16 @@ def test_prefill_fp8(backend, fmt, d):
     _run(backend, 16, 4, d, _lib.DTYPE_BF16, fmt, kv_len=[200, 40], q_len=[64, 40], chunk_pages=3, seed=d)
 
 
+@pytest.mark.parametrize("fmt", [_lib.KV_FP8_E4M3, _lib.KV_MXFP8], ids=["fp8", "mxfp8"])
+def test_prefill_rejects_f16_queries_over_8bit_kv(backend, fmt):
+    """Decode takes f16 queries over FP8 / MXFP8 pools; prefill does not
+    (DH_EUNSUPPORTED at plan creation, before any launch)."""
+    from dendrite_amd.backend import DhError
+    with pytest.raises(DhError) as e:
+        _run(backend, 16, 4, 128, _lib.DTYPE_F16, fmt, kv_len=[40], q_len=[40])
+    assert e.value.status == _lib.DH_EUNSUPPORTED
+
+
 def test_prefill_chunks_gqa_invalid_and_full(backend):
     # chunk boundaries inside and across the diagonal, interleaved GQA, an
     # INVALID id in each table, and the non-causal (full) variant
