@@ -122,6 +122,9 @@ SIGNATURES = {
     "dh_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "dh_decode_stages": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _U32, _P]),
     "dh_decode_batch_static": (_I, [_P, _P, _P, _P, _P, _P, _P]),
+    "dh_csr_workspace_size": (C.c_size_t, [C.POINTER(dh_attn_config), _U32, _U32]),
+    "dh_decode_csr": (_I, [_P, _P, C.POINTER(dh_attn_config), _U32, _P, _P, _P, _P, _P, _P, C.c_size_t, _P,
+                           _P]),
     "dh_merge_states": (_I, [_P, _P, _P, _P, _P, _P, _U32, _U32, _P]),
     "dh_gather_debug": (_I, [_P, _PU32, _U32, _U32, _P, _PU32, _P]),
     "dh_debug_e4m3_to_bf16": (_I, [_I, _P, _P, _U32, _P]),

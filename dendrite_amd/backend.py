@@ -387,6 +387,25 @@ def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream
                                  C.c_void_p(_stream_ptr(stream))))
 
 
+def csr_workspace_size(config: AttentionConfig, batch_size: int, max_total_pages: int) -> int:
+    """dh_csr_workspace_size: workspace bytes of decode_csr."""
+    return int(lib().dh_csr_workspace_size(C.byref(config.to_c()), batch_size, max_total_pages))
+
+
+def decode_csr(backend: "Backend", pool: "Pool", config: AttentionConfig, q, indices, indptr, last_page_len,
+               out, workspace, status=None, stream=None) -> None:
+    """dh_decode_csr: one decode step from device int32 CSR page tables
+    (BatchDecodeKernel::run, batch_decode.rs:86-95).  q / out [B][Hq][D];
+    indices, indptr, last_page_len (or None), status (or None): device int32
+    tensors; workspace: device uint8 of >= csr_workspace_size bytes."""
+    batch = int(indptr.numel()) - 1
+    ptr = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
+    check(lib().dh_decode_csr(backend._h, pool._h, C.byref(config.to_c()), max(batch, 0), ptr(q), ptr(indices),
+                              ptr(indptr), ptr(last_page_len), ptr(out), ptr(workspace),
+                              workspace.numel() * workspace.element_size(), ptr(status),
+                              C.c_void_p(_stream_ptr(stream))))
+
+
 class TreeDecoder:
     """Decode steps over the leaves of a TreeState (tree/state.rs) with one
     cascade plan kept current from the tree's own events.

@@ -862,7 +862,7 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
     void* ws_o = ws;
     dh::PartialLse* ws_lse = reinterpret_cast<dh::PartialLse*>(static_cast<uint8_t*>(ws) + pl->ws_lse_off);
     if (mask & 1u) {
-        dh::AttendArgs a;
+        dh::AttendArgs a{};
         a.items = pl->items;
         a.pages = pl->pages;
         a.seqslots = pl->seqslots;
@@ -886,12 +886,13 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
         a.row_len = pl->row_len;
         a.item_lim = pl->item_lim;
         a.out_direct = pl->direct ? out : nullptr;
+        a.page_limit = pool->num_pages;
         hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim,
                                                     pl->prefill, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     }
     if ((mask & 2u) && !pl->direct) {
-        dh::MergeArgs m;
+        dh::MergeArgs m{};
         m.slot_ptr = pl->slot_ptr;
         m.ws_o = ws_o;
         m.ws_lse = ws_lse;
@@ -924,6 +925,164 @@ dh_status dh_decode_batch_static(dh_backend* be, const dh_pool* pool, const dh_p
                     "(use dh_decode_batch with a workspace)", pl->ws_bytes, size_t(DH_STATIC_WORKSPACE_BYTES));
     return decode_impl(be, pool, pl, q, last_page_len, out, be->scratch, DH_STATIC_WORKSPACE_BYTES, 3u, stream,
                        true);
+}
+
+/* ------------------------------------------------- decode from device CSR */
+
+namespace {
+
+// Workspace of dh_decode_csr for `slots` partial-state slots, each section
+// 256-byte aligned: header, slot_ptr[B+1], seq_bad[B], seqslots[slots],
+// partial O [slots][Hq][D] (fp32 for f32 queries, else f16), log-sum-exps.
+struct CsrLayout {
+    size_t hdr, slot_ptr, seq_bad, seqslots, ws_o, ws_lse, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+CsrLayout csr_layout(const dh_attn_config& c, uint32_t batch, uint64_t slots) {
+    CsrLayout l;
+    const size_t eb = c.q_dtype == DH_DTYPE_F32 ? 4 : 2;
+    l.hdr = 0;
+    l.slot_ptr = align256(sizeof(dh::CsrHeader));
+    l.seq_bad = l.slot_ptr + align256(size_t(batch + 1) * 4);
+    l.seqslots = l.seq_bad + align256(size_t(batch) * 4);
+    l.ws_o = l.seqslots + align256(slots * sizeof(dh::SeqSlot));
+    l.ws_lse = l.ws_o + align256(slots * c.num_heads * c.head_dim * eb);
+    l.total = l.ws_lse + align256(slots * c.num_heads * sizeof(dh::PartialLse));
+    return l;
+}
+
+uint32_t csr_row_blocks(const dh_attn_config& c) {
+    const uint32_t r = c.num_heads / c.num_kv_heads;
+    return (r + dh::kWaveRows - 1) / dh::kWaveRows;
+}
+
+// Slots beyond the batch's own that a call uses at most (its grid covers
+// them; a larger workspace is not used past this).
+constexpr uint64_t kCsrMaxExtraSlots = 4096;
+constexpr uint32_t kCsrMaxBatch = 65536;
+
+}  // namespace
+
+size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch, uint32_t max_total_pages) {
+    if (!cfg || cfg->num_kv_heads == 0 || cfg->num_heads == 0 || batch == 0) return 0;
+    const uint64_t per = uint64_t(cfg->num_kv_heads) * csr_row_blocks(*cfg);
+    const uint64_t t = max_total_pages;
+    const uint64_t need = (t + dh::kCsrMaxChunk - 1) / dh::kCsrMaxChunk;
+    const uint64_t par = std::min((t + dh::kCsrMinChunk - 1) / dh::kCsrMinChunk,
+                                  (uint64_t(dh::kCsrTargetWaves) + per - 1) / per);
+    const uint64_t extra = std::min(kCsrMaxExtraSlots, std::max<uint64_t>(1, std::max(need, par)));
+    return csr_layout(*cfg, batch, uint64_t(batch) + extra).total;
+}
+
+dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_config* cfg, uint32_t batch,
+                        const void* q, const int32_t* indices, const int32_t* indptr,
+                        const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes, int32_t* status,
+                        void* stream) {
+    if (!be || !pool || !cfg) return fail(DH_EINVAL, "NULL argument");
+    dh_status st = validate_config(cfg);
+    if (st != DH_OK) return st;
+    st = check_pool_matches(cfg, pool);
+    if (st != DH_OK) return st;
+    if (batch == 0) return DH_OK;
+    if (batch > kCsrMaxBatch) return fail(DH_EINVAL, "batch_size %u exceeds %u", batch, kCsrMaxBatch);
+    if (!q || !out || !indptr || !indices || !ws)
+        return fail(DH_EINVAL, "q, out, indices, indptr and workspace must be device pointers");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(DH_EINVAL, "q and out must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(ws) & 255) return fail(DH_EINVAL, "workspace must be 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(indptr) | reinterpret_cast<uintptr_t>(indices) |
+         reinterpret_cast<uintptr_t>(last_page_len) | reinterpret_cast<uintptr_t>(status)) & 3)
+        return fail(DH_EINVAL, "indices, indptr, last_page_len and status must be 4-byte aligned");
+    const dh_attn_config& c = *cfg;
+    if (uint64_t(batch) * c.num_heads * c.head_dim * (c.q_dtype == DH_DTYPE_F32 ? 4u : 2u) > 0xFFFFFFFFull)
+        return fail(DH_EUNSUPPORTED, "q of %u x %u x %u exceeds 4 GiB", batch, c.num_heads, c.head_dim);
+    // Slots the workspace holds (at most kCsrMaxExtraSlots past the batch).
+    const CsrLayout one = csr_layout(c, batch, 1);
+    const size_t per_slot = sizeof(dh::SeqSlot) + size_t(c.num_heads) * sizeof(dh::PartialLse) +
+                            size_t(c.num_heads) * c.head_dim * (c.q_dtype == DH_DTYPE_F32 ? 4 : 2);
+    uint64_t slots = ws_bytes > one.total ? 1 + (ws_bytes - one.total) / per_slot : 0;
+    const uint64_t cap = uint64_t(batch) + kCsrMaxExtraSlots;
+    slots = std::min(slots, cap);
+    // The estimate ignores the sections' alignment: settle on the exact count.
+    while (slots < cap && csr_layout(c, batch, slots + 1).total <= ws_bytes) ++slots;
+    while (slots > 0 && csr_layout(c, batch, slots).total > ws_bytes) --slots;
+    if (slots <= batch)
+        return fail(DH_EINVAL, "workspace of %zu bytes holds %llu chunk slots; a batch of %u needs more than %u "
+                    "(dh_csr_workspace_size)", ws_bytes, (unsigned long long)slots, batch, batch);
+    DH_DEVICE(be->device);
+    for (const auto& [ptr, what] : {std::pair<const void*, const char*>{q, "q"}, {out, "out"}, {ws, "workspace"},
+                                    {indptr, "indptr"}, {indices, "indices"}, {last_page_len, "last_page_len"},
+                                    {status, "status"}}) {
+        if (!ptr) continue;
+        st = check_device_ptr(ptr, what);
+        if (st != DH_OK) return st;
+    }
+    const CsrLayout l = csr_layout(c, batch, slots);
+    uint8_t* w = static_cast<uint8_t*>(ws);
+    auto* hdr = reinterpret_cast<dh::CsrHeader*>(w + l.hdr);
+    auto* slot_ptr = reinterpret_cast<uint32_t*>(w + l.slot_ptr);
+    auto* seq_bad = reinterpret_cast<uint32_t*>(w + l.seq_bad);
+    auto* seqslots = reinterpret_cast<dh::SeqSlot*>(w + l.seqslots);
+    auto* ws_lse = reinterpret_cast<dh::PartialLse*>(w + l.ws_lse);
+    const uint32_t nrb = csr_row_blocks(c);
+    const uint32_t per_chunk = c.num_kv_heads * nrb;
+
+    dh::CsrPlanArgs p{};
+    p.indptr = indptr;
+    p.batch = batch;
+    p.per_chunk = per_chunk;
+    p.slot_cap = uint32_t(slots);
+    p.hdr = hdr;
+    p.slot_ptr = slot_ptr;
+    p.seq_bad = seq_bad;
+    p.seqslots = seqslots;
+    hipError_t e = hipError_t(dh::launch_csr_plan(p, stream));
+    if (e != hipSuccess) return fail(DH_EHIP, "CSR planning launch failed: %s", hipGetErrorString(e));
+
+    dh::AttendArgs a{};
+    a.pages = reinterpret_cast<const uint32_t*>(indices);
+    a.seqslots = seqslots;
+    a.q = q;
+    a.kv = pool->data;
+    a.scales = pool->scales;
+    a.last_page_len = last_page_len;
+    a.ws_o = w + l.ws_o;
+    a.ws_lse = ws_lse;
+    a.hq = c.num_heads;
+    a.hkv = c.num_kv_heads;
+    a.r = c.num_heads / c.num_kv_heads;
+    a.gqa_tiled = c.gqa_mapping == DH_GQA_TILED ? 1u : 0u;
+    const float sl = c.scale * 1.4426950408889634f;
+    a.scale_log2 = std::max(fabsf(sl), 0x1p-60f);
+    a.q_sign = sl < 0.f ? (c.q_dtype == DH_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
+    a.page_limit = pool->num_pages;
+    a.csr_indptr = indptr;
+    a.csr_slot_ptr = slot_ptr;
+    a.csr_hdr = reinterpret_cast<const uint32_t*>(hdr);
+    a.seq_bad = seq_bad;
+    a.csr_nrb = nrb;
+    // One wave per item, four per workgroup, over every slot the workspace
+    // holds; waves past the call's item count exit at once.
+    const uint64_t waves = slots * per_chunk;
+    e = hipError_t(dh::launch_attend(a, uint32_t((waves + dh::kWaves - 1) / dh::kWaves), c.q_dtype, c.kv_format,
+                                     c.head_dim, false, stream));
+    if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+
+    dh::MergeArgs m{};
+    m.slot_ptr = slot_ptr;
+    m.ws_o = w + l.ws_o;
+    m.ws_lse = ws_lse;
+    m.out = out;
+    m.batch = batch;
+    m.hq = c.num_heads;
+    m.seq_bad = seq_bad;
+    m.csr_hdr = hdr;
+    m.status = status;
+    e = hipError_t(dh::launch_merge(m, c.q_dtype, c.head_dim, stream));
+    if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
+    return DH_OK;
 }
 
 /* ------------------------------------------------------------------- merge */

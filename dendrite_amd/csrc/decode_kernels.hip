@@ -181,6 +181,36 @@ __device__ __forceinline__ uint32_t wave_item_index(const AttendArgs& a, int wav
     return a.n_group_items + (blockIdx.x - a.n_group_items) * kWaves + uint32_t(wave);
 }
 
+// Wave items on the plan path: the plan's count; on the CSR path: what the
+// CSR planning kernel of this call wrote.
+__device__ __forceinline__ uint32_t wave_item_end(const AttendArgs& a) {
+    return a.csr_hdr ? __builtin_amdgcn_readfirstlane(a.csr_hdr[1]) : a.n_group_items + a.n_wave_items;
+}
+
+// Wave item idx of a CSR call, derived from the tables: idx = (slot * hkv +
+// kv_head) * nrb + row block; slot is chunk k of sequence b, pages
+// indptr[b] + k * chunk .. (the last chunk ends at b's last page).
+__device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
+    const uint32_t nrb = a.csr_nrb, per = a.hkv * nrb;
+    const uint32_t slot = idx / per, rem = idx - slot * per;
+    const uint32_t h = rem / nrb, rb = rem - h * nrb;
+    const uint32_t b = __builtin_amdgcn_readfirstlane(a.seqslots[slot].seq);
+    const uint32_t chunk = __builtin_amdgcn_readfirstlane(a.csr_hdr[0]);
+    const uint32_t k = slot - __builtin_amdgcn_readfirstlane(a.csr_slot_ptr[b]);
+    const uint32_t p0 = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b]));
+    const uint32_t n = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b + 1])) - p0;
+    Item it;
+    it.page_off = p0 + k * chunk;
+    it.npages = min(chunk, n - k * chunk);
+    it.seq_off = slot;
+    it.row_begin = rb * kWaveRows;
+    it.nrows = min(uint32_t(kWaveRows), a.r - rb * kWaveRows);
+    it.kv_head = h;
+    it.flags = (k + 1) * chunk >= n ? kItemTail : 0u;
+    it.tail_seq = b;
+    return it;
+}
+
 // Valid tokens of page index i of an item.
 __device__ __forceinline__ int page_tokens(const Item& it, uint32_t i, int last_len) {
     if (i >= it.npages) return 0;
@@ -542,11 +572,15 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
     // would also drain the page loads in flight.
     const int lane = 16 * g + c;
     uint32_t idv[kWaveIdRegs];
+    bool bad = false;
     #pragma unroll
     for (int k = 0; k < kWaveIdRegs; ++k) {
         const uint32_t i = uint32_t(lane + 64 * k);
         idv[k] = i < np ? a.pages[it.page_off + i] : 0u;
+        bad |= idv[k] >= a.page_limit;
+        idv[k] = idv[k] < a.page_limit ? idv[k] : 0u;
     }
+    if (__ballot(bad) && a.seq_bad && lane == 0) a.seq_bad[it.tail_seq] = 1u;
     auto page_id = [&](uint32_t i) -> uint32_t {
         i = i < np ? i : np - 1;
         uint32_t r = 0;
@@ -814,7 +848,8 @@ __device__ __forceinline__ void group_item(const AttendArgs& a, const Item& it, 
     uint32_t* ids = reinterpret_cast<uint32_t*>(lds + 2 * GroupLayout<D, KVF>::STAGE);
     float* bscale = reinterpret_cast<float*>(ids + kGroupMaxPages);
     for (uint32_t i = tid; i < it.npages; i += kWaves * 64) {
-        const uint32_t pg = a.pages[it.page_off + i];
+        uint32_t pg = a.pages[it.page_off + i];
+        pg = pg < a.page_limit ? pg : 0u;
         ids[i] = pg;
         if constexpr (KVF == KVF_FP8) {
             const float* bsc = reinterpret_cast<const float*>(a.scales);
@@ -1595,7 +1630,10 @@ __device__ __forceinline__ void group_item_dma(const AttendArgs& a, const Item& 
     RowTargets<C::RT> rtg;
     dma_row_targets<D, C::RT>(a, it, wave, c, rtg);
     const int last_len = item_last_len(a, it);
-    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) ids[i] = a.pages[it.page_off + i];
+    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) {
+        const uint32_t pg = a.pages[it.page_off + i];
+        ids[i] = pg < a.page_limit ? pg : 0u;
+    }
     __syncthreads();
     // Tiles of this wave that hold rows: tiles w, w+4, ... below ceil(nrows/16).
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
@@ -1938,7 +1976,10 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
     RowTargets<C::RT> rtg;
     dma_row_targets<D, C::RT>(a, it, wave, c, rtg);
     const int last_len = item_last_len(a, it);
-    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) ids[i] = a.pages[it.page_off + i];
+    for (uint32_t i = tid; i < it.npages; i += kWaves * 64) {
+        const uint32_t pg = a.pages[it.page_off + i];
+        ids[i] = pg < a.page_limit ? pg : 0u;
+    }
     __syncthreads();
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
@@ -1962,7 +2003,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
         else group_item_dma<D, F16, false>(a, it, tid, wave, g, c);
     } else {
         const uint32_t idx = wave_item_index(a, wave);
-        if (idx < a.n_group_items + a.n_wave_items) wave_item<D, KVF, F16>(a, a.items[idx], g, c);
+        if (idx < wave_item_end(a)) wave_item<D, KVF, F16>(a, a.csr_hdr ? csr_item(a, idx) : a.items[idx], g, c);
     }
 }
 
@@ -1992,8 +2033,8 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t idx = wave_item_index(a, wave);
-    if (idx >= a.n_group_items + a.n_wave_items) return;
-    const Item it = a.items[idx];
+    if (idx >= wave_item_end(a)) return;
+    const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
 
     float qv[KQ];
     uint32_t dst[1] = {0u};
@@ -2019,9 +2060,12 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     const uint32_t* pages = a.pages + it.page_off;
     const uint64_t plane_bytes = uint64_t(kPageSize) * D * 4;
 
+    bool bad = false;
     for (uint32_t pi = 0; pi < it.npages; ++pi) {
         const int n0 = page_tokens(it, pi, last_len);
-        const uint8_t* kp = a.kv + plane_offset(pages[pi], 0, it.kv_head, a.hkv, D, 4);
+        const uint32_t pg = pages[pi];
+        bad |= pg >= a.page_limit;
+        const uint8_t* kp = a.kv + plane_offset(pg < a.page_limit ? pg : 0u, 0, it.kv_head, a.hkv, D, 4);
         const uint8_t* vp = kp + uint64_t(a.hkv) * plane_bytes;
         float kv[KQ];
         load_dwords<KQ>(reinterpret_cast<uint32_t*>(kv), kp + (c * D + g * KQ) * 4);
@@ -2065,6 +2109,7 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
                 O[0][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i][e], x[i], O[0][e], 0, 0, 0);
         }
     }
+    if (__ballot(bad) && a.seq_bad && lane == 0) a.seq_bad[it.tail_seq] = 1u;
     write_wave_partial<D, 1, false, true>(a, it, 0, 1, dst, m, l, O, g, c);
 }
 
@@ -2116,9 +2161,16 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     constexpr int U = 16;
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (a.status && blockIdx.x == 0 && threadIdx.x < 64) {   // the CSR call's status
+        uint32_t bad = 0;
+        for (uint32_t b = lane; b < a.batch; b += 64) bad |= a.seq_bad[b];
+        const bool any = __ballot(bad != 0) != 0;
+        if (lane == 0) *a.status = a.csr_hdr->overflow ? 2 : (any ? 1 : 0);   // DH_ENOMEM / DH_EINVAL / DH_OK
+    }
     if (row >= a.batch * a.hq) return;
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
-    const uint32_t s0 = a.slot_ptr[b], n = a.slot_ptr[b + 1] - s0;
+    const uint32_t s0 = a.slot_ptr[b];
+    const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
     float acc[PL];
     #pragma unroll
     for (int k = 0; k < PL; ++k) acc[k] = 0.f;
@@ -2192,6 +2244,97 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         if constexpr (OUT == 2) reinterpret_cast<float*>(a.out)[ob + k] = v;
         else if constexpr (OUT == 1) reinterpret_cast<__bf16*>(a.out)[ob + k] = (__bf16)v;
         else reinterpret_cast<_Float16*>(a.out)[ob + k] = (_Float16)v;
+    }
+}
+
+// ------------------------------------------------- decode from device CSR
+// Inclusive prefix sum of v over a workgroup of kCsrThreads threads; total
+// receives the workgroup's sum.  wsum: LDS, one word per wave.
+constexpr int kCsrThreads = 1024;
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int NW = kCsrThreads / 64;
+    v = wave_incl_scan(v, lane);
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t x = lane < NW ? wsum[lane] : 0u;
+        x = wave_incl_scan(x, lane);
+        if (lane < NW) wsum[lane] = x;
+    }
+    __syncthreads();
+    const uint32_t r = v + (wave ? wsum[wave - 1] : 0u);
+    total = wsum[NW - 1];
+    __syncthreads();
+    return r;
+}
+
+// Work decomposition of one dh_decode_csr call, on the device: sequence b's
+// pages indptr[b] .. indptr[b+1] split into chunks of `chunk` pages, chunk k
+// of b in partial-state slot slot_ptr[b] + k.  chunk is the largest of 8,
+// the size that gives about kCsrTargetWaves wave items, and the size that
+// keeps the slots within the workspace; past kCsrMaxChunk pages the tables do
+// not fit (overflow: no items, zeros out).  A sequence whose indptr entries
+// are negative or decreasing, or that has more than DH_MAX_SEQ_LEN / 16
+// pages, gets no chunk and is marked bad (zeros out, status DH_EINVAL).
+__global__ __launch_bounds__(kCsrThreads) void csr_plan_kernel(CsrPlanArgs p) {
+    __shared__ uint32_t wsum[kCsrThreads / 64];
+    const uint32_t tid = threadIdx.x;
+    constexpr uint32_t kMaxSeqPages = DH_MAX_SEQ_LEN / kPageSize;
+    auto seq_pages = [&](uint32_t b, bool& ok) -> uint32_t {
+        const int32_t p0 = p.indptr[b], p1 = p.indptr[b + 1];
+        ok = p0 >= 0 && p1 >= p0 && uint32_t(p1 - p0) <= kMaxSeqPages;
+        return ok ? uint32_t(p1 - p0) : 0u;
+    };
+    // Pass 1: pages of the valid sequences (<= 2^16 * 2^13, fits 32 bits).
+    uint32_t total = 0;
+    for (uint32_t base = 0; base < p.batch; base += kCsrThreads) {
+        bool ok = false;
+        const uint32_t n = base + tid < p.batch ? seq_pages(base + tid, ok) : 0u;
+        uint32_t t;
+        block_incl_scan(n, wsum, t);
+        total += t;
+    }
+    const uint64_t want = (uint64_t(total) * p.per_chunk + kCsrTargetWaves - 1) / kCsrTargetWaves;
+    const uint64_t fit = (uint64_t(total) + (p.slot_cap - p.batch) - 1) / (p.slot_cap - p.batch);
+    uint32_t chunk = uint32_t(max(uint64_t(kCsrMinChunk), max(want, fit)));
+    chunk = min(chunk, kCsrMaxChunk);
+    // Pass 2: chunk counts, their prefix sum, the slots' sequences.
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < p.batch; base += kCsrThreads) {
+        const uint32_t b = base + tid;
+        bool ok = false;
+        const uint32_t n = b < p.batch ? seq_pages(b, ok) : 0u;
+        const uint32_t cnt = (n + chunk - 1) / chunk;
+        uint32_t t;
+        const uint32_t first = carry + block_incl_scan(cnt, wsum, t) - cnt;
+        if (b < p.batch) {
+            p.slot_ptr[b] = first;
+            p.seq_bad[b] = ok ? 0u : 1u;
+            for (uint32_t k = 0; k < cnt && first + k < p.slot_cap; ++k)
+                p.seqslots[first + k] = SeqSlot{b, first + k};
+        }
+        carry += t;
+    }
+    const bool overflow = carry > p.slot_cap;
+    if (overflow)
+        for (uint32_t b = tid; b < p.batch; b += kCsrThreads) p.seq_bad[b] = 1u;
+    if (tid == 0) {
+        p.slot_ptr[p.batch] = overflow ? 0u : carry;
+        p.hdr->chunk = chunk;
+        p.hdr->n_items = overflow ? 0u : carry * p.per_chunk;
+        p.hdr->overflow = overflow ? 1u : 0u;
+        p.hdr->n_chunks = carry;
     }
 }
 
@@ -2349,6 +2492,12 @@ int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint3
         case 256: return launch_attend_d<256>(a, n_items, q_dtype, kvf, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+int launch_csr_plan(const CsrPlanArgs& p, void* stream) {
+    if (p.batch == 0 || p.slot_cap <= p.batch) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(csr_plan_kernel, dim3(1), dim3(kCsrThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
+    return hipGetLastError();
 }
 
 int launch_merge(const MergeArgs& a, uint32_t q_dtype, uint32_t d, void* stream) {

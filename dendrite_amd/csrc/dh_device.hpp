@@ -114,6 +114,39 @@ struct AttendArgs {
     // Prefill plans whose every row has one partial state: the items write
     // the normalised rows straight to out (no merge); null otherwise.
     void* out_direct;
+    // Pages in the pool: a page id at or past it is read as page 0 (and, on
+    // the CSR path, marks its sequence bad).  Plan ids are checked on the
+    // host, so there this never fires.
+    uint32_t page_limit;
+    // Decode from device CSR tables (dh_decode_csr): items are derived on
+    // the device from the tables (csr_item) instead of read from items;
+    // null on the plan path.
+    const int32_t* csr_indptr;
+    const uint32_t* csr_slot_ptr;
+    const uint32_t* csr_hdr;      // CsrHeader
+    uint32_t* seq_bad;            // [B] set to 1 for a sequence with a bad page id
+    uint32_t csr_nrb;             // row blocks of 16 per (chunk, kv head)
+};
+
+// What the CSR planning kernel leaves in the workspace for the attention
+// and merge kernels of the same call.
+struct CsrHeader {
+    uint32_t chunk;        // pages per chunk
+    uint32_t n_items;      // wave items (0 when the tables exceed the workspace)
+    uint32_t overflow;     // 1: more chunks than the workspace holds
+    uint32_t n_chunks;     // partial-state slots used
+};
+
+// Inputs of the CSR planning kernel (one workgroup).
+struct CsrPlanArgs {
+    const int32_t* indptr;   // [B+1], device
+    uint32_t batch;
+    uint32_t per_chunk;      // wave items per chunk: hkv * row blocks
+    uint32_t slot_cap;       // partial-state slots in the workspace (> batch)
+    CsrHeader* hdr;
+    uint32_t* slot_ptr;      // [B+1]
+    uint32_t* seq_bad;       // [B]
+    SeqSlot* seqslots;       // [slot_cap]
 };
 
 struct MergeArgs {
@@ -122,6 +155,11 @@ struct MergeArgs {
     const PartialLse* ws_lse;
     void* out;                   // [B][Hq][D]
     uint32_t batch, hq;
+    // CSR path (null otherwise): sequences marked bad get zeros, and the
+    // call's status (DH_OK / DH_EINVAL / DH_ENOMEM) goes to *status.
+    const uint32_t* seq_bad;
+    const CsrHeader* csr_hdr;
+    int32_t* status;
 };
 
 // Byte offset of the (page, plane, kv head) 16 x D block in the pool.
@@ -158,5 +196,9 @@ int launch_gather(const uint8_t* kv, const uint32_t* pages, uint32_t n_pages, ui
                   uint32_t hkv, uint32_t head_dim, uint32_t elem_bytes, uint8_t* out,
                   void* stream);
 bool attend_supported(uint32_t q_dtype, uint32_t kv_format, uint32_t head_dim);
+int launch_csr_plan(const CsrPlanArgs& p, void* stream);
+// Wave-item chunks the CSR path aims for (the planner's item target).
+constexpr uint32_t kCsrTargetWaves = 2048;
+constexpr uint32_t kCsrMinChunk = 8, kCsrMaxChunk = uint32_t(kWaveIdRegs) * 64;   // the wave item's page-id registers
 }  // namespace dh
 }

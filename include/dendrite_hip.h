@@ -373,6 +373,42 @@ dh_status dh_decode_batch(dh_backend* backend, const dh_pool* pool,
 dh_status dh_decode_batch_static(dh_backend* backend, const dh_pool* pool, const dh_plan* plan,
                                  const void* q, const int32_t* last_page_len, void* out, void* stream);
 
+/* ------------------------------------------------- decode from device CSR */
+
+/* Workspace bytes dh_decode_csr needs for batch_size sequences whose page
+ * tables hold at most max_total_pages entries together (indptr[batch] -
+ * indptr[0] <= max_total_pages).  The size grows with batch_size and with
+ * max_total_pages up to a cap (about 2048 work items' partial states), so a
+ * workspace sized for a long context serves every shorter one.  Replaces
+ * BatchDecodeKernel::workspace_size (flashinfer/batch_decode.rs:56-73). */
+size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch_size, uint32_t max_total_pages);
+
+/* One decode step from page tables that live on the device, read there on
+ * every call: no plan, no host copy, no synchronisation.  The contract of
+ * BatchDecodeKernel::run (flashinfer/batch_decode.rs:86-95):
+ *   indices       : device int32[indptr[batch]], page ids in the pool
+ *   indptr        : device int32[batch + 1], sequence b's pages are
+ *                   indices[indptr[b] .. indptr[b+1])
+ *   last_page_len : device int32[batch] or NULL, as for dh_decode_batch
+ *   q, out        : device [batch][num_heads][head_dim] of cfg->q_dtype
+ *   workspace     : device, >= dh_csr_workspace_size(cfg, batch, total) bytes
+ *   status        : device int32 or NULL; the call's last kernel writes
+ *                   DH_OK, DH_EINVAL (a page id outside the pool, a negative
+ *                   indptr entry or one below its predecessor: those
+ *                   sequences' outputs are zeros and no page outside the
+ *                   pool is read) or DH_ENOMEM (the tables need more work
+ *                   items than the workspace holds: every output is zeros).
+ * Every sequence is split into chunks of equal page count (chosen on the
+ * device from the tables' total, 8 to 256 pages) attended by one wave each
+ * and merged by log-sum-exp: a flat batch, without the shared-prefix
+ * reuse of a cascade plan.  Host checks (returned synchronously): cfg and
+ * pool agree, the pointers are device memory, the workspace holds at least
+ * batch + 1 chunks.  Three kernels on `stream`; allocates nothing. */
+dh_status dh_decode_csr(dh_backend* backend, const dh_pool* pool, const dh_attn_config* cfg,
+                        uint32_t batch_size, const void* q, const int32_t* indices,
+                        const int32_t* indptr, const int32_t* last_page_len, void* out,
+                        void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
+
 /* Stages of dh_decode_batch, for profiling: bit 0 = attention items,
  * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3.  A prefill
  * plan in which every query row is one work item's (one partial state per

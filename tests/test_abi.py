@@ -152,3 +152,22 @@ def test_tree_entry_points_take_16_token_blocks_only():
         if tpb != 16:
             assert rc == _lib.DH_EUNSUPPORTED and b"16" in C.string_at(L.dh_last_error())
         assert not plan.value
+
+
+def test_csr_workspace_size_grows_then_caps():
+    """dh_csr_workspace_size (host-only): 0 for an empty batch; grows with
+    the batch and with the tables' page count until the slot cap; a workspace
+    for many pages serves fewer."""
+    from dendrite_amd.backend import AttentionConfig, csr_workspace_size
+    cfg = AttentionConfig(32, 8, 128)
+    assert csr_workspace_size(cfg, 0, 100) == 0
+    sizes = [csr_workspace_size(cfg, 64, t) for t in (1, 8, 64, 512, 4096, 34304, 1 << 20, 1 << 24)]
+    assert all(s > 0 and s % 256 == 0 for s in sizes)
+    assert sizes == sorted(sizes)
+    assert sizes[-1] == sizes[-2] or sizes[-1] - sizes[-2] < sizes[-2]   # capped at 4096 extra slots
+    assert csr_workspace_size(cfg, 65, 34304) > sizes[5]
+    # f32 queries keep fp32 partial states: larger
+    cfg32 = AttentionConfig(32, 8, 128)
+    cfg32.q_dtype = _lib.DTYPE_F32
+    cfg32.kv_format = _lib.KV_F32
+    assert csr_workspace_size(cfg32, 64, 34304) > sizes[5]

@@ -1,0 +1,192 @@
+"""dh_decode_csr: decode from device-resident int32 CSR page tables, read on
+the device on every call (BatchDecodeKernel::run's contract,
+crates/dendrite-ffi/src/flashinfer/batch_decode.rs:86-95), against the CPU
+oracle on identical inputs, plus its error reporting: bad page ids and
+indptr entries (status DH_EINVAL, zeros for those sequences, no read outside
+the pool) and tables larger than the workspace (DH_ENOMEM, zeros).
+Tolerances as in test_gpu_decode (f32 1e-4; 16-bit / FP8 2e-2 beyond the
+output dtype's rounding)."""
+import numpy as np
+import pytest
+
+import oracle
+from dendrite_amd import _lib, workloads
+from dendrite_amd.backend import DhError, Pool, csr_workspace_size, decode_csr
+from tests._helpers import TOL, excess_err, max_abs_err, q_tensor
+
+pytestmark = pytest.mark.gpu
+
+
+class CsrRun:
+    """A workload's pages in a pool, its tables as device int32 CSR."""
+
+    def __init__(self, w, backend, pool_pages=None, ws_pages=None):
+        import torch
+        self.w = w
+        self.backend = backend
+        self.pool = Pool(backend, pool_pages or w.num_pool_pages, w.hkv, w.d, w.kv_format)
+        self.ids = w.page_ids()
+        self.data, self.scales = w.make_pages(self.ids)
+        self.pool.write_pages(self.ids, self.data, self.scales)
+        self.cfg = w.attention_config()
+        self.q_raw = w.make_q()
+        self.q = q_tensor(self.q_raw, w.q_dtype)
+        self.out = torch.empty_like(self.q)
+        self.status = torch.full((1,), -1, dtype=torch.int32, device="cuda:0")
+        total = int(w.indptr[-1]) if ws_pages is None else ws_pages
+        self.ws = torch.empty(csr_workspace_size(self.cfg, w.batch, total), dtype=torch.uint8, device="cuda:0")
+
+    def tables(self, indptr=None, indices=None, lpl=None):
+        import torch
+        w = self.w
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to("cuda:0")  # noqa: E731
+        return (dev(w.indices if indices is None else indices), dev(w.indptr if indptr is None else indptr),
+                dev(w.last_page_len if lpl is None else lpl))
+
+    def run(self, indptr=None, indices=None, lpl=None, use_lpl=True):
+        import torch
+        ix, ip, lp = self.tables(indptr, indices, lpl)
+        self.out.fill_(float("nan"))
+        decode_csr(self.backend, self.pool, self.cfg, self.q, ix, ip, lp if use_lpl else None, self.out, self.ws,
+                   self.status)
+        torch.cuda.synchronize()
+        return self.out.float().cpu().numpy(), int(self.status.item())
+
+    def reference(self, seqs=None, indptr=None, indices=None, lpl=None):
+        w = self.w
+        pv = oracle.PoolView(self.ids, self.data, self.scales, self.pool.num_pages, w.kv_format, w.hkv, w.d)
+        return oracle.decode(pv, self.q_raw, w.q_dtype, w.hq, self.cfg.scale, w.gqa_mapping,
+                             w.indptr if indptr is None else indptr, w.indices if indices is None else indices,
+                             w.last_page_len if lpl is None else lpl, seqs=seqs)
+
+
+def _check(run, got, ref, name):
+    raw, err = max_abs_err(got, ref), excess_err(got, ref, run.w.q_dtype)
+    print(f"[case] csr {name}: max abs err {raw:.3e}, beyond output rounding {err:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    assert err <= TOL[run.w.q_dtype], f"{name}: {err}"
+
+
+FORMATS = [(_lib.DTYPE_BF16, _lib.KV_BF16), (_lib.DTYPE_F16, _lib.KV_F16), (_lib.DTYPE_F32, _lib.KV_F32),
+           (_lib.DTYPE_BF16, _lib.KV_FP8_E4M3), (_lib.DTYPE_BF16, _lib.KV_MXFP8),
+           (_lib.DTYPE_F16, _lib.KV_FP8_E4M3)]
+
+
+@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256), (32, 1, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("fmt", FORMATS, ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8"])
+def test_random_trees(backend, shape, fmt):
+    """Fork trees (shared pages appear in several tables) with partial last
+    pages; (32, 1, 64) has 32 query heads per KV head, two row blocks per
+    chunk."""
+    hq, hkv, d = shape
+    w = workloads.random_tree(31, hq, hkv, d, fmt[0], fmt[1], n_leaves=10, pool_pages=512)
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    _check(run, got, run.reference(), f"tree {shape} {fmt}")
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3small", "c4small", "c5small"])
+def test_configs(backend, name):
+    w = {"c1": lambda: workloads.c1(),
+         "c2": lambda: workloads.c2(),
+         "c3small": lambda: workloads.c3(root_pages=40, levels=2, level_pages=3, pool_pages=4096),
+         "c4small": lambda: workloads.c4(n_seqs=24, tmin=40, tmax=700, pool_pages=4096),
+         "c5small": lambda: workloads.c5(requests=2, prefix_pages=40, beams=4, suffix_pages=5, pool_pages=2048)}[name]()
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    _check(run, got, run.reference(), name)
+
+
+def test_c3_full_flat(backend):
+    """The headline tree read flat from device tables: every leaf's 536
+    pages, all 64 leaves against the oracle."""
+    w = workloads.c3()
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    _check(run, got, run.reference(), "c3 full")
+
+
+def test_empty_sequences_and_full_last_pages(backend):
+    tables = [[], [3, 4, 5], [], [7], [6, 2]]
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 16, last_page_len=[1, 5, 16, 0, 9])
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    assert np.all(got[0] == 0) and np.all(got[2] == 0)
+    _check(run, got, run.reference(), "empty + lpl")
+    # last_page_len NULL: every page full
+    got, st = run.run(use_lpl=False)
+    assert st == _lib.DH_OK
+    _check(run, got, run.reference(lpl=np.full(5, 16, np.int32)), "lpl NULL")
+
+
+def test_bad_ids_and_indptr_zero_their_sequences(backend):
+    """A page id outside the pool (or negative) and a decreasing indptr make
+    their sequences' outputs zero and the status DH_EINVAL; the other
+    sequences are exact and nothing outside the pool is read."""
+    tables = [[1, 2, 3], [4, 5], [6, 7, 8, 9], [10]]
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 16, last_page_len=[3, 7, 16, 2])
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    good = run.reference()
+    _check(run, got, good, "valid tables")
+    for bad_id in (16, 1 << 30, -5):
+        ix = w.indices.astype(np.int64).copy()
+        ix[3] = bad_id                       # sequence 1's first page
+        got, st = run.run(indices=ix)
+        assert st == _lib.DH_EINVAL, bad_id
+        assert np.all(got[1] == 0)
+        keep = [0, 2, 3]
+        _check(run, got[keep], good[keep], f"bad id {bad_id}")
+    ip = w.indptr.astype(np.int64).copy()
+    ip[2] = ip[1] - 1                        # sequence 1 ends before it starts
+    got, st = run.run(indptr=ip)
+    assert st == _lib.DH_EINVAL
+    assert np.all(got[1] == 0)
+    # the valid tables again: the status and outputs come back
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    _check(run, got, good, "valid again")
+
+
+def test_tables_larger_than_the_workspace(backend):
+    """A workspace sized for a few pages holds batch + 1 chunk slots: tables
+    that need more chunks of 256 pages leave every output zero with status
+    DH_ENOMEM; a workspace below batch + 1 slots is refused on the host."""
+    import torch
+    tables = [list(range(1, 600)), [700]]
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 1024)
+    run = CsrRun(w, backend, ws_pages=1)
+    got, st = run.run()
+    assert st == _lib.DH_ENOMEM
+    assert np.all(got == 0)
+    ix, ip, lp = run.tables()
+    small = torch.empty(256, dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(DhError) as e:
+        decode_csr(backend, run.pool, run.cfg, run.q, ix, ip, lp, run.out, small)
+    assert e.value.status == _lib.DH_EINVAL
+
+
+def test_tables_change_between_calls(backend):
+    """One workspace, tables that grow and shrink between calls: nothing of
+    an earlier call's decomposition leaks into the next."""
+    w = workloads.c2(branches=4, prefix_pages=60, suffix_pages=6, pool_pages=512)
+    run = CsrRun(w, backend, ws_pages=2000)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    _check(run, got, run.reference(), "c2 reduced")
+    for cut in (1, 17, 45):
+        keep = [b for b in range(w.batch)]
+        tabs = [list(w.seq_pages(b))[:max(1, len(w.seq_pages(b)) - cut * (b + 1) % 50)] for b in keep]
+        ip = np.concatenate([[0], np.cumsum([len(t) for t in tabs])]).astype(np.int64)
+        ix = np.concatenate(tabs).astype(np.int64)
+        lpl = np.array([(3 * b + cut) % 16 + 1 for b in keep], np.int32)
+        got, st = run.run(indptr=ip, indices=ix, lpl=lpl)
+        assert st == _lib.DH_OK
+        _check(run, got, run.reference(indptr=ip.astype(np.uint32), indices=ix.astype(np.uint32), lpl=lpl),
+               f"cut {cut}")
