@@ -159,6 +159,134 @@ def bench_prefill(args):
                       "steps": args.steps, "warmup": args.warmup}), flush=True)
 
 
+def bench_trait(args):
+    """--trait: one decode step through HipBackend.decode_batch, the
+    AttentionBackend path (host BlockTables in, the plan cached across calls
+    and patched at page boundaries), on C3 with every leaf growing one token
+    per step, against the raw dh_decode_batch step of one fixed plan over the
+    same tables.  The new tokens' K/V are pre-written (the engine's
+    append_kv is not part of the step): growth updates the tables and the
+    backend's token counts only.  Each step is measured from a synchronised
+    start: host time of the call, GPU span of what it enqueued (events
+    around the call), and call-to-completion latency."""
+    import torch
+    from dendrite_amd import workloads
+    from dendrite_amd.backend import DecodePlan, HipBackend, decode_batch, raw_to_tensor
+    from dendrite_amd.cache import BlockTable
+    w = workloads.c3()
+    B, H, D = w.batch, w.hq, w.d
+    total_steps = args.steps + args.warmup
+    spares_n = B * (total_steps // 16 + 2)
+    num_pages = w.num_pool_pages + spares_n
+    be = HipBackend(num_pages=num_pages, num_kv_heads=w.hkv, head_dim=D, kv_format=w.kv_format)
+    ids = np.concatenate([w.page_ids(), np.arange(w.num_pool_pages, num_pages, dtype=np.uint32)])
+    for c0 in range(0, len(ids), 8192):
+        data, scales = w.make_pages(ids[c0:c0 + 8192])
+        be.pool.write_pages(ids[c0:c0 + 8192], data, scales)
+    for p in w.page_ids():
+        be.page_len[int(p)] = 16
+    tables, last, pos = [], [], []
+    for b in range(B):
+        pages = [int(x) for x in w.seq_pages(b)]
+        tables.append(BlockTable.from_blocks(pages, num_tokens=w.seq_len(b)))
+        last.append(pages[-1])
+        pos.append(w.seq_len(b))
+        be.page_len[pages[-1]] = w.seq_len(b) - 16 * (len(pages) - 1)
+    cfg = w.attention_config()
+    q = raw_to_tensor(w.make_q(), w.q_dtype)
+    queries = [q[i].view(1, H, 1, D) for i in range(B)]
+    spare = iter(range(w.num_pool_pages, num_pages))
+
+    def grow():
+        for i, t in enumerate(tables):
+            if pos[i] % 16 == 0:
+                last[i] = next(spare)
+                t.push(last[i])
+                be.page_len[last[i]] = 1
+            else:
+                be.page_len[last[i]] += 1
+            t.add_tokens(1)
+            pos[i] += 1
+
+    def raw_plan():
+        indptr, indices, lpl = be._csr(tables)
+        plan = DecodePlan(be.backend, _trait_cfg(be, cfg, q.dtype), be.pool, indptr, indices, cascade=True)
+        return plan, torch.from_numpy(lpl).cuda()
+
+    for _ in range(args.warmup):
+        be.decode_batch(queries, tables, cfg)
+        grow()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    host, gpu, lat = [], [], []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        be.decode_batch(queries, tables, cfg)
+        ev1.record()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        host.append(t1 - t0)
+        lat.append(t2 - t0)
+        gpu.append(ev0.elapsed_time(ev1) * 1e-3)
+        grow()
+    st = dict(built=be.plans_built, patched=be.plans_patched, reused=be.plans_reused)
+    # The raw step on the final tables: one fixed plan, back-to-back and
+    # from a synchronised start like the trait calls.
+    t0 = time.perf_counter()
+    plan, lpl = raw_plan()
+    plan_s = time.perf_counter() - t0
+    out = torch.empty_like(q)
+    ws = plan.workspace()
+    for _ in range(10):
+        decode_batch(plan, q, out, ws, lpl)
+    torch.cuda.synchronize()
+    rlat, rgpu = [], []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        decode_batch(plan, q, out, ws, lpl)
+        ev1.record()
+        torch.cuda.synchronize()
+        rlat.append(time.perf_counter() - t0)
+        rgpu.append(ev0.elapsed_time(ev1) * 1e-3)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        decode_batch(plan, q, out, ws, lpl)
+    torch.cuda.synchronize()
+    raw_b2b = (time.perf_counter() - t0) / args.steps
+    med = lambda x: float(np.median(x)) * 1e6  # noqa: E731
+    log(f"[bench] trait: host {med(host):.1f} us/call, GPU span {med(gpu):.1f} us, latency {med(lat):.1f} us; "
+        f"raw: GPU span {med(rgpu):.1f} us, latency {med(rlat):.1f} us, back-to-back {raw_b2b * 1e6:.1f} us; "
+        f"plans {st}; a new plan costs {plan_s * 1e6:.0f} us")
+    print(json.dumps({"metric": "trait decode step (HipBackend.decode_batch, C3 growing 1 token/step)",
+                      "unit": "us", "higher_is_better": False,
+                      "trait_host_us_per_call": round(med(host), 2),
+                      "trait_gpu_span_us": round(med(gpu), 2),
+                      "trait_latency_us": round(med(lat), 2),
+                      "raw_gpu_span_us": round(med(rgpu), 2),
+                      "raw_latency_us": round(med(rlat), 2),
+                      "raw_back_to_back_us": round(raw_b2b * 1e6, 2),
+                      "new_plan_us": round(plan_s * 1e6, 1),
+                      "plans": st, "steps": args.steps, "warmup": args.warmup,
+                      "config": {"workload": "c3", "batch": B, "growth": "1 token per leaf per step"}}),
+          flush=True)
+
+
+def _trait_cfg(be, config, qdt):
+    from dendrite_amd.backend import AttentionConfig, dtype_code
+    cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
+    cfg.scale = config.scale
+    cfg.gqa_mapping = config.gqa_mapping
+    cfg.q_dtype = dtype_code(qdt)
+    cfg.kv_format = be.pool.kv_format
+    return cfg
+
+
 def bench_plan_timing(args):
     """Host cost of keeping a decode plan current: dh_plan_create (planning
     and upload) against dh_plan_update with one appended page for each of
@@ -239,6 +367,9 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--trait", action="store_true",
+                    help="only measure the AttentionBackend path (HipBackend.decode_batch) on C3 with tables "
+                         "growing one token per step, against the raw step")
     ap.add_argument("--plan-timing", action="store_true",
                     help="only time dh_plan_create against dh_plan_update (32 appended pages) on the host")
     ap.add_argument("--prefill", default="", metavar="CTX:NEW[xB]",
@@ -271,6 +402,9 @@ def main():
 
     from dendrite_amd.backend import Backend, DecodePlan, Pool, decode_batch, raw_to_tensor
 
+    if args.trait:
+        bench_trait(args)
+        return
     if args.plan_timing:
         bench_plan_timing(args)
         return

@@ -500,6 +500,153 @@ class TreeDecoder:
         return out
 
 
+def _list_events(old: np.ndarray, new: np.ndarray):
+    """dh_plan_update events turning page list old into new: [] when equal;
+    appends when new extends old; a replaced last page (copy-on-write)
+    followed by appends.  None for anything else (a new plan)."""
+    n = min(len(old), len(new))
+    same = int(np.argmin(old[:n] == new[:n])) if n and not (old[:n] == new[:n]).all() else n
+    if same == len(old) and len(new) >= len(old):
+        return [(_lib.PLAN_APPEND, int(p)) for p in new[same:]]
+    if len(old) and same == len(old) - 1 and len(new) >= len(old):
+        return [(_lib.PLAN_REPLACE_LAST, int(new[same]))] + [(_lib.PLAN_APPEND, int(p)) for p in new[same + 1:]]
+    return None
+
+
+def _batched(queries, shape, dev):
+    """(the queries as one [B][H][D] tensor, whether it is a view): a view
+    when they already are consecutive rows of one buffer, else a stacked
+    copy."""
+    torch = _torch()
+    q0 = queries[0]
+    B, H, D = shape
+    step = H * D
+    if q0.is_cuda and q0.is_contiguous():
+        base = q0.data_ptr()
+        es = q0.element_size()
+        if all(x.is_contiguous() and x.dtype == q0.dtype and x.data_ptr() == base + i * step * es
+               and x.numel() == step for i, x in enumerate(queries)):
+            st = q0.untyped_storage()
+            off = q0.storage_offset()
+            if off + B * step <= st.nbytes() // es:
+                return torch.empty(0, dtype=q0.dtype, device=q0.device).set_(st, off, (B, H, D)), True
+    return torch.stack([x.reshape(H, D) for x in queries]).to(dev).contiguous(), False
+
+
+class _PageLens(dict):
+    """block id -> tokens stored, kept in step with `array` (int32 over the
+    pool) and `epoch` (moves when a block starts or stops holding tokens)."""
+
+    def __init__(self, num_pages: int):
+        super().__init__()
+        self.array = np.zeros(num_pages, dtype=np.int32)
+        self.epoch = 0
+
+    def _mirror(self, block, n) -> None:
+        b = int(block)
+        old = int(self.array[b]) if 0 <= b < len(self.array) else int(dict.get(self, b, 0))
+        if 0 <= b < len(self.array):
+            self.array[b] = n
+        if (old > 0) != (n > 0):
+            self.epoch += 1
+
+    def __setitem__(self, block, n) -> None:
+        self._mirror(block, int(n))
+        super().__setitem__(block, n)
+
+    def __delitem__(self, block) -> None:
+        self._mirror(block, 0)
+        super().__delitem__(block)
+
+    def pop(self, block, *default):
+        if block in self:
+            self._mirror(block, 0)
+        return super().pop(block, *default)
+
+    def clear(self) -> None:
+        super().clear()
+        self.array[:] = 0
+        self.epoch += 1
+
+    def update(self, *a, **kw) -> None:
+        for k, v in dict(*a, **kw).items():
+            self[k] = v
+
+    def setdefault(self, block, n=None):
+        if block not in self:
+            self[block] = n
+        return self[block]
+
+
+class _PlanCache:
+    """HipBackend's decode plan and what goes with it across calls: the key
+    it was built for, each sequence's page list and last page, the
+    workspace, and a ring of pinned host buffers for last_page_len (a
+    buffer is refilled only after the copy that read it has run)."""
+
+    RING = 4
+
+    def __init__(self):
+        self.key = None
+        self.mut = -1
+        self.tables = []
+        self.cfg = None
+        self.plan = None
+        self.ws = None
+        self.kept = []
+        self.last_ids = np.zeros(0, dtype=np.int64)
+        self.last_empty = np.zeros(0, dtype=bool)
+        self._queries = None     # the last call's query list and its batched tensor
+        self._qbatch = None
+        self._retired = []   # (plan, event): freed once the work that read it has run
+        self._host = []
+        self._dev = []
+        self._done = []
+        self._i = 0
+
+    def replace(self, plan) -> None:
+        """Makes plan current; the previous one lives until the work already
+        queued on the current stream (which may read it) has run."""
+        torch = _torch()
+        self._retired = [(p, e) for p, e in self._retired if not e.query()]
+        if self.plan is not None:
+            ev = torch.cuda.Event()
+            ev.record()
+            self._retired.append((self.plan, ev))
+        self.plan = plan
+
+    def new_batch(self, batch: int, device: int) -> None:
+        torch = _torch()
+        if self._host and self._host[0].numel() == batch:
+            return
+        self._host = [torch.empty(batch, dtype=torch.int32, pin_memory=True) for _ in range(self.RING)]
+        self._dev = [torch.empty(batch, dtype=torch.int32, device=f"cuda:{device}") for _ in range(self.RING)]
+        self._done = [torch.cuda.Event() for _ in range(self.RING)]
+        self._used = [False] * self.RING
+
+    def query_batch(self, queries, shape, dev):
+        """_batched, skipped when the call passes the very tensors of the
+        previous call and those were a view of one buffer (a serving loop's
+        persistent query rows: the view sees their new contents)."""
+        prev = self._queries
+        if prev is not None and len(prev) == len(queries) and all(a is b for a, b in zip(prev, queries)):
+            return self._qbatch
+        q, view = _batched(queries, shape, dev)
+        self._queries, self._qbatch = (list(queries), q) if view else (None, None)
+        return q
+
+    def last_page_lens(self, values):
+        i = self._i
+        self._i = (i + 1) % self.RING
+        if self._used[i]:
+            self._done[i].synchronize()
+        self._host[i].numpy()[:] = values
+        self._dev[i].copy_(self._host[i], non_blocking=True)
+        self._done[i].record()
+        self._used[i] = True
+        return self._dev[i]
+
+
 class HipBackend:
     """AttentionBackend (backend.rs:61-97) on the HIP decode path.
 
@@ -515,11 +662,25 @@ class HipBackend:
         self.backend = Backend(device)
         self.pool = Pool(self.backend, num_pages, num_kv_heads, head_dim, kv_format)
         self.cascade = cascade
-        self.page_len: dict[int, int] = {}
+        # Tokens stored per block (a dict, mirrored into an array over the
+        # pool with an epoch that moves whenever a block starts or stops
+        # holding tokens: what decode's page lists depend on, beyond the
+        # tables themselves).
+        self.page_len = _PageLens(num_pages)
         # FP8 pools: the f32 tokens of each page still being filled, so an
         # append re-quantises the page from all its tokens (a block scale
         # covers the whole page); dropped once the page holds 16 tokens.
         self._shadow: dict = {}
+        self._plans = _PlanCache()
+        self.plans_built = 0
+        self.plans_patched = 0
+        self.plans_reused = 0
+
+    def _set_len(self, block: int, n: int) -> None:
+        if n > 0:
+            self.page_len[block] = n
+        else:
+            self.page_len.pop(block, None)
 
     @classmethod
     def new(cls, **kw) -> "HipBackend":
@@ -582,20 +743,20 @@ class HipBackend:
                           f"so offset {off} would leave tokens {stored}..{off - 1} unwritten")
         if self.pool.kv_format in (_lib.KV_FP8_E4M3, _lib.KV_MXFP8):
             n = self._append_quantised(int(block), off, key, value)
-            self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + n)
+            self._set_len(int(block), max(self.page_len.get(int(block), 0), off + n))
             return
         k = self._kv_np(key)
         v = self._kv_np(value)
         if k.shape[0] != self.pool.num_kv_heads or k.shape[2] != self.pool.head_dim:
             raise DhError(_lib.DH_EINVAL, f"key shape {tuple(key.shape)} does not match the pool")
         self.pool.write_tokens(int(block), off, k, v)
-        self.page_len[int(block)] = max(self.page_len.get(int(block), 0), off + k.shape[1])
+        self._set_len(int(block), max(self.page_len.get(int(block), 0), off + k.shape[1]))
 
     def store_kv(self, block_id: int, key, value) -> None:
         """ReferenceBackend::store_kv (backend.rs:140-143): the block's entry
         becomes key / value ([1, num_kv_heads, n, head_dim], n <= 16), from
         token 0 (overwrite, as the reference's map insert)."""
-        self.page_len.pop(int(block_id), None)
+        self._set_len(int(block_id), 0)
         self._shadow.pop(int(block_id), None)
         self.append_kv(key, value, BlockTable.from_blocks([int(block_id)]), 0)
 
@@ -623,24 +784,82 @@ class HipBackend:
         self.page_len.clear()
         self._shadow.clear()
 
+    def _kept(self, t: BlockTable) -> np.ndarray:
+        """The table's pages decode reads: valid blocks holding tokens, in
+        order; every one but the last must be full."""
+        ids = t.block_ids()
+        lens = self.page_len.array
+        inpool = ids < len(lens)
+        kept = ids[inpool & (lens[np.where(inpool, ids, 0)] > 0)]
+        if len(kept) > 1:
+            short = lens[kept[:-1]] != _lib.PAGE_SIZE
+            if short.any():
+                b = int(kept[:-1][short][0])
+                raise DhError(_lib.DH_EUNSUPPORTED,
+                              f"block {b} holds {self.page_len[b]} tokens but is not the last "
+                              "stored block of its table")
+        return kept
+
     def _csr(self, tables: Sequence[BlockTable]):
-        indptr, indices, lpl = [0], [], []
-        for t in tables:
-            kept = [int(b) for b in t.blocks() if b.is_valid() and self.page_len.get(int(b), 0) > 0]
-            for b in kept[:-1]:
-                if self.page_len[b] != _lib.PAGE_SIZE:
-                    raise DhError(_lib.DH_EUNSUPPORTED,
-                                  f"block {b} holds {self.page_len[b]} tokens but is not the last "
-                                  "stored block of its table")
-            indices.extend(kept)
-            indptr.append(len(indices))
-            lpl.append(self.page_len[kept[-1]] if kept else _lib.PAGE_SIZE)
-        return (np.array(indptr, dtype=np.uint32), np.array(indices, dtype=np.uint32),
-                np.array(lpl, dtype=np.int32))
+        kept = [self._kept(t) for t in tables]
+        indptr = np.concatenate([[0], np.cumsum([len(k) for k in kept])]).astype(np.uint32)
+        indices = np.concatenate(kept).astype(np.uint32) if kept else np.zeros(0, np.uint32)
+        lpl = np.array([self.page_len[int(k[-1])] if len(k) else _lib.PAGE_SIZE for k in kept], dtype=np.int32)
+        return indptr, indices, lpl
+
+    def _plan_for(self, tables: Sequence[BlockTable], cfg: AttentionConfig, cfg_key):
+        """The decode plan of these tables: the cached one when neither the
+        tables (uid, version) nor the set of stored blocks changed; patched
+        in place (dh_plan_update) when each page list only gained pages at
+        its end or had its last page replaced; else a new plan."""
+        from .cache import block_table_mutations
+        c = self._plans
+        mut = block_table_mutations()
+        if (c.plan is not None and c.mut == mut and c.key[0] == cfg_key and c.key[3] == self.page_len.epoch
+                and len(c.tables) == len(tables) and all(a is b for a, b in zip(c.tables, tables))):
+            self.plans_reused += 1     # no table changed anywhere since the plan's key was taken
+            return c
+        key = (cfg_key, tuple(t.uid for t in tables), tuple(t.version for t in tables), self.page_len.epoch)
+        if c.plan is not None and c.key == key:
+            c.mut, c.tables = mut, list(tables)
+            self.plans_reused += 1
+            return c
+        kept = [self._kept(t) for t in tables]
+        events = None
+        if c.plan is not None and c.key[0] == cfg_key and c.key[1] == key[1]:
+            events = []
+            for i, (old, new) in enumerate(zip(c.kept, kept)):
+                ev = _list_events(old, new)
+                if ev is None:
+                    events = None
+                    break
+                events.extend((i, op, pid) for op, pid in ev)
+        if events is not None and (not events or c.plan.update(events)):
+            self.plans_patched += bool(events)
+            self.plans_reused += not events
+        else:
+            indptr = np.concatenate([[0], np.cumsum([len(k) for k in kept])]).astype(np.uint32)
+            indices = np.concatenate(kept).astype(np.uint32) if kept else np.zeros(0, np.uint32)
+            c.replace(DecodePlan(self.backend, cfg, self.pool, indptr, indices, cascade=self.cascade))
+            if c.ws is None or c.ws.numel() < c.plan.workspace_size:
+                c.ws = c.plan.workspace()
+            c.new_batch(len(tables), self.backend.device)
+            self.plans_built += 1
+        c.key = key
+        c.mut, c.tables = mut, list(tables)
+        c.kept = kept
+        c.last_ids = np.array([int(k[-1]) if len(k) else 0 for k in kept], dtype=np.int64)
+        c.last_empty = np.array([len(k) == 0 for k in kept], dtype=bool)
+        return c
 
     def decode_batch(self, queries, block_tables: Sequence[BlockTable], config: AttentionConfig):
         """queries: list of [1, num_heads, 1, head_dim] tensors; returns the
-        list of outputs, same shape and dtype (backend.rs:267-283)."""
+        outputs as one tensor [B, 1, num_heads, 1, head_dim] of the queries'
+        dtype, whose row i is query i's output (indexed and iterated like the
+        reference's Vec<Tensor>, backend.rs:267-283).  The plan is cached
+        across calls (see _plan_for); the sequences' last-page lengths go up
+        through pinned host buffers.  Results are ordered on the current
+        stream (no host synchronisation)."""
         torch = _torch()
         if len(queries) != len(block_tables):
             raise DhError(_lib.DH_EINVAL, "queries and block_tables differ in length")
@@ -648,21 +867,25 @@ class HipBackend:
             return []
         dev = f"cuda:{self.backend.device}"
         qdt = queries[0].dtype
-        cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
-        cfg.scale = config.scale
-        cfg.sliding_window = config.sliding_window
-        cfg.gqa_mapping = config.gqa_mapping
-        cfg.q_dtype = dtype_code(qdt)
-        cfg.kv_format = self.pool.kv_format
-        indptr, indices, lpl = self._csr(block_tables)
-        plan = DecodePlan(self.backend, cfg, self.pool, indptr, indices, cascade=self.cascade)
-        q = torch.stack([x.reshape(config.num_heads, config.head_dim) for x in queries]).to(dev).contiguous()
-        out = torch.empty_like(q)
-        lp = torch.from_numpy(lpl).to(dev)
-        ws = plan.workspace()
-        decode_batch(plan, q, out, ws, lp)
-        torch.cuda.synchronize(dev)
-        return [out[i].reshape(1, config.num_heads, 1, config.head_dim) for i in range(len(queries))]
+        cfg_key = (config.num_heads, config.num_kv_heads, config.head_dim, config.scale, config.gqa_mapping, qdt)
+        cfg = self._plans.cfg if self._plans.key is not None and self._plans.key[0] == cfg_key else None
+        if cfg is None:
+            cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
+            cfg.scale = config.scale
+            cfg.sliding_window = config.sliding_window
+            cfg.gqa_mapping = config.gqa_mapping
+            cfg.q_dtype = dtype_code(qdt)
+            cfg.kv_format = self.pool.kv_format
+        c = self._plan_for(block_tables, cfg, cfg_key)
+        c.cfg = cfg
+        B, H, D = len(queries), config.num_heads, config.head_dim
+        q = c.query_batch(queries, (B, H, D), dev)
+        lens = self.page_len.array[c.last_ids]
+        lens[c.last_empty] = _lib.PAGE_SIZE
+        lpl = c.last_page_lens(lens)
+        out = torch.empty((B, H, D), dtype=qdt, device=dev)
+        decode_batch(c.plan, q, out, c.ws, lpl)
+        return out.view(B, 1, H, 1, D)
 
     def decode(self, query, block_table: BlockTable, config: AttentionConfig):
         """backend.rs:206-265."""

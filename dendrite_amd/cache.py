@@ -10,8 +10,11 @@ The implementation is the C++ block model inside libdendrite_hip.so.
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 from dataclasses import dataclass
 from typing import Optional
+
+import numpy as np
 
 from . import _lib
 from ._lib import DhError, check, lib
@@ -49,8 +52,23 @@ NodeId.ROOT = NodeId(_lib.ROOT_NODE)
 NodeId.INVALID = NodeId(_lib.INVALID_NODE)
 
 
+_table_uids = itertools.count(1)
+# Bumped by every change of any table's block list (a cheap "did anything
+# change" check before looking at each table's version).
+_mutations = [0]
+
+
+def block_table_mutations() -> int:
+    return _mutations[0]
+
+
 class BlockTable:
-    """Logical -> physical block mapping of one sequence."""
+    """Logical -> physical block mapping of one sequence.
+
+    uid (unique per object for the process) and version (bumped by every
+    change of the block list: push, set, clear) let a caller cache what it
+    derived from the list, e.g. HipBackend's decode plans; neither exists in
+    the reference, whose decode re-reads every table on every call."""
 
     def __init__(self, tokens_per_block: int = 16, _handle=None):
         self._h = C.c_void_p()
@@ -60,6 +78,8 @@ class BlockTable:
         else:
             check(lib().dh_block_table_create(tokens_per_block, C.byref(self._h)))
         self.tokens_per_block = tokens_per_block
+        self.uid = next(_table_uids)
+        self.version = 0
 
     @classmethod
     def new(cls, tokens_per_block: int = 16) -> "BlockTable":
@@ -94,9 +114,13 @@ class BlockTable:
 
     def push(self, block_id: int) -> None:
         check(lib().dh_block_table_push(self._h, int(block_id)))
+        self.version += 1
+        _mutations[0] += 1
 
     def set(self, logical_idx: int, block_id: int) -> None:
         check(lib().dh_block_table_set(self._h, logical_idx, int(block_id)))
+        self.version += 1
+        _mutations[0] += 1
 
     def set_num_tokens(self, count: int) -> None:
         check(lib().dh_block_table_set_num_tokens(self._h, count))
@@ -110,6 +134,14 @@ class BlockTable:
         lib().dh_block_table_blocks(self._h, buf, n)
         return [BlockId(buf[i]) for i in range(n)]
 
+    def block_ids(self) -> np.ndarray:
+        """blocks() as a uint32 array (one copy out of the C model)."""
+        n = lib().dh_block_table_blocks(self._h, None, 0)
+        out = np.empty(n, dtype=np.uint32)
+        if n:
+            lib().dh_block_table_blocks(self._h, out.ctypes.data_as(_lib._PU32), n)
+        return out
+
     def needs_new_block(self) -> bool:
         return bool(lib().dh_block_table_needs_new_block(self._h))
 
@@ -120,6 +152,8 @@ class BlockTable:
 
     def clear(self) -> None:
         check(lib().dh_block_table_clear(self._h))
+        self.version += 1
+        _mutations[0] += 1
 
     @classmethod
     def from_blocks(cls, ids, num_tokens: Optional[int] = None, tokens_per_block: int = 16):

@@ -340,3 +340,65 @@ def test_append_kv_leaves_no_unwritten_tokens(kvf):
         out = be.decode(q, table, cfg).cpu().reshape(hkv, d).numpy()
         want = 0.5 * (v16 + v17).reshape(hkv, d).numpy()
         assert np.max(np.abs(out - want)) < 1e-6
+
+
+def test_trait_decode_reuses_and_patches_its_plan():
+    """decode_batch through the trait with tables that grow one token per
+    step (append_kv + add_tokens; a new block every 16 tokens) and a
+    copy-on-write of a last block: the cached plan is reused between page
+    boundaries, patched in place at them (dh_plan_update) and rebuilt only
+    when a list changes elsewhere; every step matches the oracle."""
+    import torch
+    hq, hkv, d = 16, 4, 64
+    be = HipBackend(num_pages=256, num_kv_heads=hkv, head_dim=d)
+    cfg = AttentionConfig(hq, hkv, d)
+    prefix = [1, 2, 3]
+    for i, b in enumerate(prefix):
+        _store_block(be, b, 100 + 2 * i, hkv=hkv, d=d)
+    tables, pos, nxt = [], [], [10]
+    for leaf in range(4):
+        n0 = 5 + 3 * leaf
+        t = BlockTable.from_blocks(prefix + [nxt[0]], num_tokens=48 + n0)
+        be.append_kv(_randn((1, hkv, n0, d), 200 + 2 * leaf), _randn((1, hkv, n0, d), 201 + 2 * leaf), t, 48)
+        tables.append(t)
+        pos.append(48 + n0)
+        nxt[0] += 1
+    base = _randn((4, hq, d), 7).to(torch.bfloat16).cuda()
+    queries = [base[i].view(1, hq, 1, d) for i in range(4)]
+
+    def check(step):
+        outs = be.decode_batch(queries, tables, cfg)
+        got = np.stack([o.float().cpu().reshape(hq, d).numpy() for o in outs])
+        want = _oracle_for(be, tables, [q.cpu() for q in queries], cfg)
+        err = float(np.max(np.abs(got - want)))
+        print(f"[case] trait step {step}: max abs err {err:.3e}", flush=True)
+        assert err < 2e-2, step
+
+    seed = 300
+    for step in range(40):
+        check(step)
+        for i, t in enumerate(tables):
+            if pos[i] % 16 == 0:
+                t.push(nxt[0])
+                nxt[0] += 1
+            seed += 2
+            be.append_kv(_randn((1, hkv, 1, d), seed), _randn((1, hkv, 1, d), seed + 1), t, pos[i])
+            t.add_tokens(1)
+            pos[i] += 1
+    built, patched, reused = be.plans_built, be.plans_patched, be.plans_reused
+    print(f"[case] trait plans: built {built}, patched {patched}, reused {reused}", flush=True)
+    # leaves start 5, 8, 11, 14 tokens into their page: each crosses two or
+    # three page boundaries in 40 steps, at different steps
+    assert built == 1 and patched >= 8 and built + patched + reused == 40
+    # copy-on-write of leaf 0's partial last block: REPLACE_LAST
+    last = int(tables[0].block_ids()[-1])
+    be.pool.copy_page(last, nxt[0])
+    be.page_len[nxt[0]] = be.page_len[last]
+    tables[0].set(tables[0].num_blocks() - 1, nxt[0])
+    check("cow")
+    assert be.plans_built == 1 and be.plans_patched == patched + 1
+    # a middle block replaced: a new plan
+    tables[1].set(1, 4)
+    _store_block(be, 4, 400, hkv=hkv, d=d)
+    check("middle")
+    assert be.plans_built == 2
