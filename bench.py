@@ -90,15 +90,28 @@ def cpu_baseline(w, budget_s: float = 12.0):
 
 
 def measured_traffic(workload: str):
-    """HBM bytes per launch of the attention kernel from the committed
+    """(HBM bytes per launch of the attention kernel from the committed
     rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy
-    calibration), or None when no summary for this workload exists."""
+    calibration), note).  The summary records a SHA-256 over the sources
+    that shape the kernel's traffic; when these files differ now, the
+    figure belongs to other code: bytes None, and the note says so."""
+    import hashlib
     path = os.path.join(ROOT, "profiles", f"attend16_{workload}_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         t = json.load(f)
-    return t.get("hbm_bytes_per_launch")
+    h = hashlib.sha256()
+    try:
+        for src in t.get("sources", []):
+            with open(os.path.join(ROOT, src), "rb") as f:
+                h.update(f.read())
+    except OSError:
+        return None, "counter summary's sources not found"
+    if not t.get("sources") or h.hexdigest() != t.get("sources_sha256"):
+        return None, (f"stale: counters taken at {t.get('commit', '?')[:12]} on other sources "
+                      f"({t.get('hbm_bytes_per_launch')} B then)")
+    return t.get("hbm_bytes_per_launch"), f"counters taken at {t.get('commit', '?')[:12]} on these sources"
 
 
 def bench_prefill(args):
@@ -484,7 +497,7 @@ def main():
     log(f"[bench] step {ms_step * 1e3:.2f} us (attend {ms_attend * 1e3:.2f} us, merge {ms_merge * 1e3:.2f} us)"
         f"; single-step median {np.median(per) * 1e3:.2f} us")
 
-    traffic = measured_traffic(w0.name)
+    traffic, traffic_note = measured_traffic(w0.name)
     gbs = alg / (ms_step * 1e-3) / 1e9
     attend_gbs = alg_attend / (ms_attend * 1e-3) / 1e9
     result = {
@@ -523,6 +536,7 @@ def main():
             "unit": "GB/s",
             "frac": round(attend_gbs / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_note": traffic_note,
             "avg_launch_us": round(ms_attend * 1e3, 3),
             "merge_launch_us": round(ms_merge * 1e3, 3),
             "mfma_tflops": round(w0.flops() / (ms_attend * 1e-3) / 1e12, 2),

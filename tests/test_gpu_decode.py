@@ -45,9 +45,11 @@ def test_c3_small_tree(backend, cascade):
     _check(w, backend, cascade=cascade)
 
 
-def test_c3_full_tree_sampled(backend):
+def test_c3_full_tree_all_leaves(backend):
+    """The headline configuration at full size: all 64 leaves against the
+    oracle."""
     w = workloads.c3()
-    run, _ = _check(w, backend, seqs=[0, 5, 21, 42, 63])
+    run, _ = _check(w, backend)
     st = run.plan.stats()
     # Every page of the tree is read once per KV head per step.
     assert st["page_reads"] == st["unique_pages"] == 1184
@@ -58,9 +60,15 @@ def test_c4_small_fp8(backend):
     _check(w, backend)
 
 
-def test_c4_full_fp8_sampled(backend):
+def test_c4_full_fp8_forked_and_others(backend):
+    """C4 at full size: every forked sequence (each 8th shares a prefix with
+    its predecessor) and the sequences it forked from, plus others: 72 of
+    256 against the oracle."""
     w = workloads.c4()
-    _check(w, backend, seqs=[0, 7, 15, 100, 255])
+    forked = list(range(7, w.batch, 8))
+    seqs = sorted(set(forked + [f - 1 for f in forked] + [0, 1, 2, 100, 150, 200, 254, 13]))
+    assert len(seqs) >= 32
+    _check(w, backend, seqs=seqs)
 
 
 def test_c5_small_mxfp8(backend):

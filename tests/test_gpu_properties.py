@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from dendrite_amd import _lib, workloads
-from tests._helpers import TOL, GpuRun, excess_err
+from tests._helpers import max_abs_err, TOL, GpuRun, excess_err
 
 pytestmark = pytest.mark.gpu
 
@@ -85,13 +85,18 @@ def test_maximum_sequence_length(backend):
     assert excess_err(got, run.reference(), w.q_dtype) <= TOL[w.q_dtype]
 
 
-def test_c5_full_sampled(backend):
+def test_c5_full_one_leaf_per_request(backend):
+    """C5 at full size: one leaf of each of the 32 requests (beam r % 16 of
+    request r) and the last leaf, 33 of 512, against the oracle."""
     w = workloads.c5()
     print(f"[case] c5 full batch={w.batch}", flush=True)
     run = GpuRun(w, backend)
     got = run.run()
-    seqs = [0, 17, 255, 511]
-    err = excess_err(got[np.asarray(seqs)], run.reference(seqs=seqs), w.q_dtype)
-    print(f"[case] c5 full: error beyond output rounding {err:.3e}", flush=True)
+    seqs = sorted(set([16 * r + r % 16 for r in range(32)] + [w.batch - 1]))
+    ref = run.reference(seqs=seqs)
+    sub = got[np.asarray(seqs)]
+    raw, err = max_abs_err(sub, ref), excess_err(sub, ref, w.q_dtype)
+    print(f"[case] c5 full ({len(seqs)} leaves): max abs err {raw:.3e}, beyond output rounding {err:.3e}",
+          flush=True)
     assert np.all(np.isfinite(got))
     assert err <= TOL[w.q_dtype]
