@@ -380,6 +380,8 @@ def main():
     ap.add_argument("--shared-chunk", type=int, default=0)
     ap.add_argument("--private-chunk", type=int, default=0)
     ap.add_argument("--target-items", type=int, default=0)
+    ap.add_argument("--flat", action="store_true", help="plan option: no cascade (every sequence alone)")
+    ap.add_argument("--no-direct", action="store_true", help="plan option: never a direct (merge-free) plan")
     ap.add_argument("--trait", action="store_true",
                     help="only measure the AttentionBackend path (HipBackend.decode_batch) on C3 with tables "
                          "growing one token per step, against the raw step")
@@ -445,9 +447,10 @@ def main():
             del data, scales
             if len(ids) > chunk:
                 log(f"[bench] pages {min(c0 + chunk, len(ids))}/{len(ids)} written")
-        plan = DecodePlan(be, w.attention_config(), pool, w.indptr, w.indices, cascade=True,
+        plan = DecodePlan(be, w.attention_config(), pool, w.indptr, w.indices, cascade=not args.flat,
                           shared_chunk_pages=args.shared_chunk,
-                          private_chunk_pages=args.private_chunk, target_items=args.target_items)
+                          private_chunk_pages=args.private_chunk, target_items=args.target_items,
+                          direct=not args.no_direct)
         plans.append(plan)
         q = raw_to_tensor(w.make_q(), w.q_dtype)
         qs.append(q)

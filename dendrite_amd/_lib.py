@@ -31,6 +31,8 @@ GQA_TILED, GQA_INTERLEAVED = 0, 1
 # plan flags
 PLAN_FLAT, PLAN_CASCADE = 0, 1
 PLAN_APPEND, PLAN_REPLACE_LAST = 0, 1
+# dh_plan_options.direct
+DIRECT_AUTO, DIRECT_OFF = 0, 1
 
 PAGE_SIZE = 16
 STATIC_WORKSPACE_BYTES = 32 << 20   # DH_STATIC_WORKSPACE_BYTES
@@ -57,14 +59,15 @@ class dh_attn_config(C.Structure):
 
 class dh_plan_options(C.Structure):
     _fields_ = [("shared_chunk_pages", C.c_uint32), ("private_chunk_pages", C.c_uint32),
-                ("target_items", C.c_uint32), ("reserved", C.c_uint32 * 5)]
+                ("target_items", C.c_uint32), ("direct", C.c_uint32),
+                ("reserved", C.c_uint32 * 4)]
 
 
 class dh_plan_stats(C.Structure):
     _fields_ = [("batch_size", C.c_uint32), ("num_segments", C.c_uint32),
                 ("num_shared_segments", C.c_uint32), ("num_items", C.c_uint32),
                 ("num_tasks", C.c_uint32), ("num_group_items", C.c_uint32),
-                ("num_partials", C.c_uint32), ("unique_pages", C.c_uint64),
+                ("num_partials", C.c_uint32), ("direct", C.c_uint32), ("unique_pages", C.c_uint64),
                 ("page_reads", C.c_uint64), ("total_pages", C.c_uint64)]
 
 

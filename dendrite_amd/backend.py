@@ -246,7 +246,7 @@ class DecodePlan:
 
     def __init__(self, backend: Backend, config: AttentionConfig, pool: Pool, indptr, indices,
                  cascade: bool = True, shared_chunk_pages: int = 0, private_chunk_pages: int = 0,
-                 target_items: int = 0):
+                 target_items: int = 0, direct: bool = True):
         self.backend = backend
         self.pool = pool
         self.config = config
@@ -257,6 +257,7 @@ class DecodePlan:
         opt.shared_chunk_pages = shared_chunk_pages
         opt.private_chunk_pages = private_chunk_pages
         opt.target_items = target_items
+        opt.direct = _lib.DIRECT_AUTO if direct else _lib.DIRECT_OFF
         self._c = config.to_c()
         self._h = C.c_void_p()
         self._destroy = lib().dh_plan_destroy
@@ -321,7 +322,7 @@ class DecodePlan:
 
 def plan_inspect(config: AttentionConfig, num_pool_pages: int, indptr, indices, cascade: bool = True,
                  shared_chunk_pages: int = 0, private_chunk_pages: int = 0,
-                 target_items: int = 0) -> dict:
+                 target_items: int = 0, direct: bool = True) -> dict:
     """Host-only planning (dh_plan_inspect): the plan's stats, items, page list
     and (sequence, slot) pairs, without a device."""
     ip = np.ascontiguousarray(indptr, dtype=np.uint32)
@@ -331,6 +332,7 @@ def plan_inspect(config: AttentionConfig, num_pool_pages: int, indptr, indices, 
     opt.shared_chunk_pages = shared_chunk_pages
     opt.private_chunk_pages = private_chunk_pages
     opt.target_items = target_items
+    opt.direct = _lib.DIRECT_AUTO if direct else _lib.DIRECT_OFF
     c = config.to_c()
     flags = _lib.PLAN_CASCADE if cascade else _lib.PLAN_FLAT
     ni, npg, nss = C.c_uint32(), C.c_uint32(), C.c_uint32()

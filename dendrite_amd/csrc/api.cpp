@@ -498,6 +498,8 @@ static dh_status host_plan(const dh_attn_config* cfg, uint32_t num_pool_pages, c
         in.shared_chunk_pages = opt->shared_chunk_pages;
         in.private_chunk_pages = opt->private_chunk_pages;
         in.target_items = opt->target_items;
+        if (opt->direct > DH_DIRECT_OFF) return fail(DH_EINVAL, "unknown direct option %u", opt->direct);
+        in.direct_ok = opt->direct != DH_DIRECT_OFF;
     }
     std::string err;
     const int rc = dh::build_plan(in, hp, err);
@@ -514,6 +516,7 @@ static void fill_stats(const dh::HostPlan& hp, uint32_t batch, dh_plan_stats* s)
     s->num_tasks = uint32_t(hp.tasks.size());
     s->num_group_items = hp.num_group_items;
     s->num_partials = hp.num_slots;
+    s->direct = hp.direct ? 1u : 0u;
     s->unique_pages = hp.unique_pages;
     s->page_reads = hp.page_reads;
     s->total_pages = hp.total_pages;
@@ -609,7 +612,7 @@ static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh
         pl->tail_item_ptr = hp.tail_item_ptr;
         pl->tail_items = hp.tail_items;
     }
-    pl->direct = prefill;
+    pl->direct = prefill || hp.direct;
     for (uint32_t v = 0; prefill && v < batch; ++v)
         if (hp.slot_ptr[v + 1] - hp.slot_ptr[v] != 1) pl->direct = false;
     pl->items_word = o_items / sizeof(uint32_t);
@@ -885,8 +888,13 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
         a.n_wave_items = pl->n_wave_items;
         a.row_len = pl->row_len;
         a.item_lim = pl->item_lim;
-        a.out_direct = pl->direct ? out : nullptr;
+        a.out_direct = pl->direct && pl->prefill ? out : nullptr;
         a.page_limit = pool->num_pages;
+        if (pl->direct && !pl->prefill) {   // direct decode plan: wave tasks merge their own rows
+            a.wave_direct = 1u;
+            a.slot_ptr = pl->slot_ptr;
+            a.out = out;
+        }
         hipError_t e = hipError_t(dh::launch_attend(a, pl->n_tasks, c.q_dtype, c.kv_format, c.head_dim,
                                                     pl->prefill, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));

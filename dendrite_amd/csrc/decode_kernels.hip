@@ -334,9 +334,10 @@ __device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, ui
 }
 
 // ---------------------------------------------------------------- pair math
-// Scores of a page pair for NRT row tiles: s[rt][p] = S^T tile of page p.
+// Scores of a page pair for NRT row tiles: s[rt][p] = S^T tile of page p
+// (k0 / k1: the two pages' K operands).
 template <int D, bool F16, int NRT, int RT>
-__device__ __forceinline__ void pair_scores(const uint32_t (&kop)[2][D / 32][4],
+__device__ __forceinline__ void pair_scores(const uint32_t (&k0)[D / 32][4], const uint32_t (&k1)[D / 32][4],
                                             const uint32_t (&qB)[RT][D / 32][4], f4 (&s)[RT][2]) {
     constexpr int KB = D / 32;
     #pragma unroll
@@ -345,8 +346,8 @@ __device__ __forceinline__ void pair_scores(const uint32_t (&kop)[2][D / 32][4],
         s[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-            s[rt][0] = mma16<F16>(kop[0][kb], qB[rt][kb], s[rt][0]);
-            s[rt][1] = mma16<F16>(kop[1][kb], qB[rt][kb], s[rt][1]);
+            s[rt][0] = mma16<F16>(k0[kb], qB[rt][kb], s[rt][0]);
+            s[rt][1] = mma16<F16>(k1[kb], qB[rt][kb], s[rt][1]);
         }
     }
 }
@@ -354,8 +355,8 @@ __device__ __forceinline__ void pair_scores(const uint32_t (&kop)[2][D / 32][4],
 // Online softmax of a pair's scores and O^T += V^T P^T.  f0/f1: scale_log2
 // times the pages' K scales; v0s/v1s: the pages' V scales (1 unless FP8
 // block-scaled); n0/n1: valid tokens of the two pages (n1 = 0: no page).
-// vop holds, per page, the V rows of tokens 4g+j (bf16/f16 dwords, zero for
-// invalid tokens).
+// v0 / v1 hold, per page, the V rows of tokens 4g+j (bf16/f16 dwords, zero
+// for invalid tokens).
 //
 // Running max: a row's reference max m only moves when some score exceeds it
 // by more than kLazy (so every exp2 stays <= 2^kLazy).  Whether that happens
@@ -428,7 +429,8 @@ __device__ __forceinline__ void pair_softmax(const f4 (&s)[RT][2], int n0, int n
 }
 
 template <int D, bool F16, int NRT, int RT, bool BLOCK_SCALE>
-__device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint32_t (&vop)[2][4][D / 32],
+__device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint32_t (&v0)[4][D / 32],
+                                                const uint32_t (&v1)[4][D / 32],
                                                 int n0, int n1, float f0, float f1, float v0s, float v1s,
                                                 float (&m)[RT], f4 (&L)[RT], f4 (&O)[RT][D / 16], int g) {
     constexpr int EPL = D / 16;
@@ -441,12 +443,24 @@ __device__ __forceinline__ void pair_softmax_pv(const f4 (&s)[RT][2], const uint
         const int w = e >> 1;
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
         uint32_t vA[4];
-        vA[0] = __builtin_amdgcn_perm(vop[0][1][w], vop[0][0][w], sel);
-        vA[1] = __builtin_amdgcn_perm(vop[0][3][w], vop[0][2][w], sel);
-        vA[2] = __builtin_amdgcn_perm(vop[1][1][w], vop[1][0][w], sel);
-        vA[3] = __builtin_amdgcn_perm(vop[1][3][w], vop[1][2][w], sel);
+        vA[0] = __builtin_amdgcn_perm(v0[1][w], v0[0][w], sel);
+        vA[1] = __builtin_amdgcn_perm(v0[3][w], v0[2][w], sel);
+        vA[2] = __builtin_amdgcn_perm(v1[1][w], v1[0][w], sel);
+        vA[3] = __builtin_amdgcn_perm(v1[3][w], v1[2][w], sel);
         #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16<F16>(vA, pB[rt], O[rt][e]);
+    }
+}
+
+// Zeroes, in a lane's 16-bit V rows (tokens 4g+j), the tokens at or past
+// nt (their probabilities are zero; garbage there must not reach O).
+template <int D>
+__device__ __forceinline__ void mask_v_rows(uint32_t (&v)[4][D / 32], int g, int nt) {
+    #pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool ok = 4 * g + j < nt;
+        #pragma unroll
+        for (int w = 0; w < D / 32; ++w) v[j][w] = ok ? v[j][w] : 0u;
     }
 }
 
@@ -593,7 +607,9 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
     // DEPTH page pairs in flight: buffer p % DEPTH holds pair p; once pair
     // p's K (then V) has been consumed, its K (V) registers take pair
     // p + DEPTH's.  Two for E4M3 pages at head_dim <= 128 (a pair is 32
-    // registers); one where a second pair would not fit beside the math.
+    // registers).  16-bit pages keep one: two fit in registers at head_dim
+    // 128, but on C3 the extra traffic of the tails slowed the shared-prefix
+    // items beside them more than it sped the tails (30.4 against 29.2 µs).
     constexpr int DEPTH = (KVF == KVF_FP8 && D <= 128) ? 2 : 1;
     PageRaw<D, KVF> pr[DEPTH][2];
     float ks[DEPTH][2], vs[DEPTH][2];
@@ -624,25 +640,39 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
         const uint32_t i0 = 2 * pi;
         const int n0 = page_tokens(it, i0, last_len);
         const int n1 = page_tokens(it, i0 + 1, last_len);
-        uint32_t kop[2][KB][4];
-        k_operand<D, KVF, F16>(pr[buf][0], kop[0]);
-        k_operand<D, KVF, F16>(pr[buf][1], kop[1]);
         f4 sc[1][2];
-        pair_scores<D, F16, 1, 1>(kop, qB, sc);
         const float f0 = a.scale_log2 * ks[buf][0], f1 = a.scale_log2 * ks[buf][1];
         const float v0s = vs[buf][0], v1s = vs[buf][1];
         const bool refill = pi + DEPTH < npairs;
-        if (refill) load_pair(buf, pi + DEPTH, true);
-        uint32_t vop[2][4][D / 32];
         const bool full = (n0 == kPageSize) && (n1 == kPageSize);
-        if (full) {
-            v_operand<D, KVF, F16>(pr[buf][0], g, kPageSize, vop[0]);
-            v_operand<D, KVF, F16>(pr[buf][1], g, kPageSize, vop[1]);
+        if constexpr (!PageRaw<D, KVF>::FP8) {
+            // 16-bit pages are their own MFMA operands (no copies).  V past
+            // a page's valid tokens is zeroed in place (the registers are
+            // refilled after the PV products).
+            pair_scores<D, F16, 1, 1>(pr[buf][0].k, pr[buf][1].k, qB, sc);
+            if (refill) load_pair(buf, pi + DEPTH, true);
+            if (!full) {
+                mask_v_rows<D>(pr[buf][0].v, g, n0);
+                mask_v_rows<D>(pr[buf][1].v, g, n1);
+            }
+            pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(sc, pr[buf][0].v, pr[buf][1].v, n0, n1, f0, f1, v0s, v1s,
+                                                       m, L, O, g);
         } else {
-            v_operand<D, KVF, F16>(pr[buf][0], g, n0, vop[0]);
-            v_operand<D, KVF, F16>(pr[buf][1], g, n1, vop[1]);
+            uint32_t kop[2][KB][4];
+            k_operand<D, KVF, F16>(pr[buf][0], kop[0]);
+            k_operand<D, KVF, F16>(pr[buf][1], kop[1]);
+            pair_scores<D, F16, 1, 1>(kop[0], kop[1], qB, sc);
+            if (refill) load_pair(buf, pi + DEPTH, true);
+            uint32_t vop[2][4][D / 32];
+            if (full) {
+                v_operand<D, KVF, F16>(pr[buf][0], g, kPageSize, vop[0]);
+                v_operand<D, KVF, F16>(pr[buf][1], g, kPageSize, vop[1]);
+            } else {
+                v_operand<D, KVF, F16>(pr[buf][0], g, n0, vop[0]);
+                v_operand<D, KVF, F16>(pr[buf][1], g, n1, vop[1]);
+            }
+            pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(sc, vop[0], vop[1], n0, n1, f0, f1, v0s, v1s, m, L, O, g);
         }
-        pair_softmax_pv<D, F16, 1, 1, BLOCK_SCALE>(sc, vop, n0, n1, f0, f1, v0s, v1s, m, L, O, g);
         if (refill) load_pair(buf, pi + DEPTH, false);
     };
     for (uint32_t pi = 0; pi < npairs; pi += DEPTH) {
@@ -810,8 +840,9 @@ __device__ __forceinline__ void group_loop(const AttendArgs& a, const Item& it, 
             uint32_t vop[2][4][D / 32];
             group_operands<D, KVF, F16>(stage, g, c, n0, n1, kop, vop);
             f4 s[RT][2];
-            pair_scores<D, F16, NRT, RT>(kop, qB, s);
-            pair_softmax_pv<D, F16, NRT, RT, BLOCK_SCALE>(s, vop, n0, n1, f0, f1, v0s, v1s, m, Lsum, O, g);
+            pair_scores<D, F16, NRT, RT>(kop[0], kop[1], qB, s);
+            pair_softmax_pv<D, F16, NRT, RT, BLOCK_SCALE>(s, vop[0], vop[1], n0, n1, f0, f1, v0s, v1s, m, Lsum,
+                                                          O, g);
         }
     };
 
@@ -1990,6 +2021,32 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
 
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
+template <int D, uint32_t OUT>
+__device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
+                                          uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane);
+
+// Direct decode plans: after its waves wrote their partial states, the
+// workgroup merges its rows (one (sequence, KV head, row block): the rows of
+// its first item) over the sequence's slots and writes out.  The states are
+// read back through the cache right after they were written: a workgroup
+// fence and barrier order the writes of every wave before the reads.
+template <int D, uint32_t OUT>
+__device__ __forceinline__ void wave_task_merge(const AttendArgs& a, int wave, int lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const Item it = uniform_item(a.items[a.n_group_items + (blockIdx.x - a.n_group_items) * kWaves]);
+    for (uint32_t row = uint32_t(wave); row < it.nrows; row += kWaves) {
+        uint32_t seq, slot, qh;
+        row_target(a, it, row, seq, slot, qh);
+        seq = __builtin_amdgcn_readfirstlane(seq);
+        qh = __builtin_amdgcn_readfirstlane(qh);
+        const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.slot_ptr[seq]);
+        const uint32_t n = __builtin_amdgcn_readfirstlane(a.slot_ptr[seq + 1]) - s0;
+        merge_row<D, OUT>(a.ws_o, a.ws_lse, a.out, a.hq, seq, qh, s0, n, lane);
+    }
+}
+
 template <int D, uint32_t KVF, bool F16>
 __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
@@ -2003,7 +2060,11 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
         else group_item_dma<D, F16, false>(a, it, tid, wave, g, c);
     } else {
         const uint32_t idx = wave_item_index(a, wave);
-        if (idx < wave_item_end(a)) wave_item<D, KVF, F16>(a, a.csr_hdr ? csr_item(a, idx) : a.items[idx], g, c);
+        if (idx < wave_item_end(a)) {
+            const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
+            if (it.npages) wave_item<D, KVF, F16>(a, it, g, c);   // direct tasks pad with empty items
+        }
+        if (a.wave_direct) wave_task_merge<D, F16 ? 0u : 1u>(a, wave, tid & 63);
     }
 }
 
@@ -2026,15 +2087,11 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill16_kernel(Attend
 // step, 16 rows per wave.
 //   S^T: A = K[token c][g*D/4 + kb], B = Q[row c][g*D/4 + kb], kb < D/4.
 //   O^T: for token group i: A = V[4g+i][c*EPL + e], B = P[row c][4g+i].
+// One wave item of attend32_kernel.
 template <int D>
-__global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
+__device__ __forceinline__ void attend32_item(const AttendArgs& a, const Item& it, int lane, int g, int c) {
     constexpr int KQ = D / 4;
     constexpr int EPL = D / 16;
-    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t idx = wave_item_index(a, wave);
-    if (idx >= wave_item_end(a)) return;
-    const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
 
     float qv[KQ];
     uint32_t dst[1] = {0u};
@@ -2058,59 +2115,87 @@ __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
 
     const int last_len = item_last_len(a, it);
     const uint32_t* pages = a.pages + it.page_off;
+    const uint32_t np = it.npages;
     const uint64_t plane_bytes = uint64_t(kPageSize) * D * 4;
 
+    // DEPTH pages in flight: buffer p % DEPTH holds page p; once page p is
+    // consumed its registers take page p + DEPTH.  Two at head_dim 64 (32
+    // registers a page); one above (64 or 128), where a second page would
+    // cost occupancy.
+    constexpr int DEPTH = D <= 64 ? 2 : 1;
+    float kb[DEPTH][KQ];
+    float vb[DEPTH][4][EPL];
     bool bad = false;
-    for (uint32_t pi = 0; pi < it.npages; ++pi) {
-        const int n0 = page_tokens(it, pi, last_len);
+    auto load = [&](int buf, uint32_t pi) {
         const uint32_t pg = pages[pi];
         bad |= pg >= a.page_limit;
         const uint8_t* kp = a.kv + plane_offset(pg < a.page_limit ? pg : 0u, 0, it.kv_head, a.hkv, D, 4);
         const uint8_t* vp = kp + uint64_t(a.hkv) * plane_bytes;
-        float kv[KQ];
-        load_dwords<KQ>(reinterpret_cast<uint32_t*>(kv), kp + (c * D + g * KQ) * 4);
-        float vv[4][EPL];
+        load_dwords<KQ>(reinterpret_cast<uint32_t*>(kb[buf]), kp + (c * D + g * KQ) * 4);
         #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            load_dwords<EPL>(reinterpret_cast<uint32_t*>(vv[i]), vp + ((4 * g + i) * D + c * EPL) * 4);
-            if (4 * g + i >= n0) {
-                #pragma unroll
-                for (int e = 0; e < EPL; ++e) vv[i][e] = 0.f;
-            }
-        }
-        f4 s = {0.f, 0.f, 0.f, 0.f};
-        #pragma unroll
-        for (int k = 0; k < KQ; ++k) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[k], qv[k], s, 0, 0, 0);
-        float x[4];
-        float mx = kNegInf;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[i] = (4 * g + i < n0) ? s[i] * a.scale_log2 : kNegInf;
-            mx = fmaxf(mx, x[i]);
-        }
-        mx = rowgroup_max(mx);
-        const float mnew = fmaxf(m[0], mx);
-        const float muse = (mnew == kNegInf) ? 0.f : mnew;
-        const float alpha = fast_exp2(m[0] - muse);
-        m[0] = mnew;
-        float ps = 0.f;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[i] = fast_exp2(x[i] - muse);
-            ps += x[i];
-        }
-        l[0] = l[0] * alpha + ps;
-        #pragma unroll
-        for (int e = 0; e < EPL; ++e) O[0][e] *= alpha;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i)
+            load_dwords<EPL>(reinterpret_cast<uint32_t*>(vb[buf][i]), vp + ((4 * g + i) * D + c * EPL) * 4);
+    };
+    #pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        if (uint32_t(d) < np) load(d, d);
+    #pragma unroll 1
+    for (uint32_t p0 = 0; p0 < np; p0 += DEPTH) {
+        static_for<0, DEPTH>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t pi = p0 + j;
+            if (pi >= np) return;
+            const int n0 = page_tokens(it, pi, last_len);
+            f4 s = {0.f, 0.f, 0.f, 0.f};
             #pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                O[0][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i][e], x[i], O[0][e], 0, 0, 0);
-        }
+            for (int k = 0; k < KQ; ++k) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[j][k], qv[k], s, 0, 0, 0);
+            float x[4];
+            float mx = kNegInf;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = (4 * g + i < n0) ? s[i] * a.scale_log2 : kNegInf;
+                mx = fmaxf(mx, x[i]);
+            }
+            mx = rowgroup_max(mx);
+            const float mnew = fmaxf(m[0], mx);
+            const float muse = (mnew == kNegInf) ? 0.f : mnew;
+            const float alpha = fast_exp2(m[0] - muse);
+            m[0] = mnew;
+            float ps = 0.f;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = fast_exp2(x[i] - muse);
+                ps += x[i];
+            }
+            l[0] = l[0] * alpha + ps;
+            #pragma unroll
+            for (int e = 0; e < EPL; ++e) O[0][e] *= alpha;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // V past the page's valid tokens: zero (its weight is zero,
+                // garbage there must not reach O).
+                const bool ok = 4 * g + i < n0;
+                #pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    O[0][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(ok ? vb[j][i][e] : 0.f, x[i], O[0][e], 0, 0, 0);
+            }
+            if (pi + DEPTH < np) load(j, pi + DEPTH);
+        });
     }
     if (__ballot(bad) && a.seq_bad && lane == 0) a.seq_bad[it.tail_seq] = 1u;
     write_wave_partial<D, 1, false, true>(a, it, 0, 1, dst, m, l, O, g, c);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t idx = wave_item_index(a, wave);
+    if (idx < wave_item_end(a)) {
+        const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
+        if (it.npages) attend32_item<D>(a, it, lane, g, c);   // direct tasks pad with empty items
+    }
+    if (a.wave_direct) wave_task_merge<D, 2u>(a, wave, lane);
 }
 
 // ------------------------------------------------------------------ merge
@@ -2155,22 +2240,13 @@ __device__ __forceinline__ void load_partial(const void* ws, uint64_t e, float (
     }
 }
 
+// One wave merges output row (b, qh) over partial slots s0 .. s0 + n - 1
+// (no slot: zeros).
 template <int D, uint32_t OUT>
-__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+__device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
+                                          uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane) {
     constexpr int PL = D / 64;
     constexpr int U = 16;
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (a.status && blockIdx.x == 0 && threadIdx.x < 64) {   // the CSR call's status
-        uint32_t bad = 0;
-        for (uint32_t b = lane; b < a.batch; b += 64) bad |= a.seq_bad[b];
-        const bool any = __ballot(bad != 0) != 0;
-        if (lane == 0) *a.status = a.csr_hdr->overflow ? 2 : (any ? 1 : 0);   // DH_ENOMEM / DH_EINVAL / DH_OK
-    }
-    if (row >= a.batch * a.hq) return;
-    const uint32_t b = row / a.hq, qh = row - b * a.hq;
-    const uint32_t s0 = a.slot_ptr[b];
-    const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
     float acc[PL];
     #pragma unroll
     for (int k = 0; k < PL; ++k) acc[k] = 0.f;
@@ -2179,12 +2255,12 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         // One pass: the log-sum-exps and the first U partial rows are loaded
         // together (neither depends on the other), so a row with up to U
         // partial states costs one memory round trip after slot_ptr.
-        const PartialLse pk = uint32_t(lane) < n ? a.ws_lse[uint64_t(s0 + lane) * a.hq + qh]
+        const PartialLse pk = uint32_t(lane) < n ? ws_lse[uint64_t(s0 + lane) * hq + qh]
                                                  : PartialLse{kNegInf, 0.f};
         float v[U][PL];
         #pragma unroll
         for (int u = 0; u < U; ++u)
-            load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + min(uint32_t(u), n - 1)) * a.hq + qh) * D + lane * PL, v[u]);
+            load_partial<OUT, PL>(ws_o, (uint64_t(s0 + min(uint32_t(u), n - 1)) * hq + qh) * D + lane * PL, v[u]);
         const float M = wave_max(pk.lse);
         if (M != kNegInf) {
             const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
@@ -2194,7 +2270,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
                 if (j0) {
                     #pragma unroll
                     for (int u = 0; u < U; ++u)
-                        load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + min(j0 + u, n - 1)) * a.hq + qh) * D + lane * PL,
+                        load_partial<OUT, PL>(ws_o, (uint64_t(s0 + min(j0 + u, n - 1)) * hq + qh) * D + lane * PL,
                                               v[u]);
                 }
                 #pragma unroll
@@ -2207,13 +2283,13 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         }
     } else if (n > 64) {
         float M = kNegInf;
-        for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, a.ws_lse[uint64_t(s0 + k) * a.hq + qh].lse);
+        for (uint32_t k = lane; k < n; k += 64) M = fmaxf(M, ws_lse[uint64_t(s0 + k) * hq + qh].lse);
         M = wave_max(M);
         if (M != kNegInf) {
             for (uint32_t base = 0; base < n; base += 64) {
                 // Weight of slot base + lane, then the slots' O rows in groups of U.
                 const uint32_t k = base + lane;
-                const PartialLse pk = k < n ? a.ws_lse[uint64_t(s0 + k) * a.hq + qh] : PartialLse{kNegInf, 0.f};
+                const PartialLse pk = k < n ? ws_lse[uint64_t(s0 + k) * hq + qh] : PartialLse{kNegInf, 0.f};
                 const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
                 W += wk;
                 const float wo = __builtin_amdgcn_ldexpf(wk, int(pk.k));   // weight of the stored (scaled) O
@@ -2223,7 +2299,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
                     #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const uint32_t j = min(j0 + u, cnt - 1);
-                        load_partial<OUT, PL>(a.ws_o, (uint64_t(s0 + base + j) * a.hq + qh) * D + lane * PL, v[u]);
+                        load_partial<OUT, PL>(ws_o, (uint64_t(s0 + base + j) * hq + qh) * D + lane * PL, v[u]);
                     }
                     #pragma unroll
                     for (int u = 0; u < U; ++u) {
@@ -2237,14 +2313,31 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     }
     W = wave_sum(W);
     const float inv = W > 0.f ? 1.f / W : 0.f;
-    const uint64_t ob = (uint64_t(b) * a.hq + qh) * D + lane * PL;
+    const uint64_t ob = (uint64_t(b) * hq + qh) * D + lane * PL;
     #pragma unroll
     for (int k = 0; k < PL; ++k) {
         const float v = acc[k] * inv;
-        if constexpr (OUT == 2) reinterpret_cast<float*>(a.out)[ob + k] = v;
-        else if constexpr (OUT == 1) reinterpret_cast<__bf16*>(a.out)[ob + k] = (__bf16)v;
-        else reinterpret_cast<_Float16*>(a.out)[ob + k] = (_Float16)v;
+        if constexpr (OUT == 2) reinterpret_cast<float*>(out)[ob + k] = v;
+        else if constexpr (OUT == 1) reinterpret_cast<__bf16*>(out)[ob + k] = (__bf16)v;
+        else reinterpret_cast<_Float16*>(out)[ob + k] = (_Float16)v;
     }
+}
+
+template <int D, uint32_t OUT>
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (a.status && blockIdx.x == 0 && threadIdx.x < 64) {   // the CSR call's status
+        uint32_t bad = 0;
+        for (uint32_t b = lane; b < a.batch; b += 64) bad |= a.seq_bad[b];
+        const bool any = __ballot(bad != 0) != 0;
+        if (lane == 0) *a.status = a.csr_hdr->overflow ? 2 : (any ? 1 : 0);   // DH_ENOMEM / DH_EINVAL / DH_OK
+    }
+    if (row >= a.batch * a.hq) return;
+    const uint32_t b = row / a.hq, qh = row - b * a.hq;
+    const uint32_t s0 = a.slot_ptr[b];
+    const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
+    merge_row<D, OUT>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
 }
 
 // ------------------------------------------------- decode from device CSR

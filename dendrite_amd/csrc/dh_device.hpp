@@ -126,6 +126,12 @@ struct AttendArgs {
     const uint32_t* csr_hdr;      // CsrHeader
     uint32_t* seq_bad;            // [B] set to 1 for a sequence with a bad page id
     uint32_t csr_nrb;             // row blocks of 16 per (chunk, kv head)
+    // Direct decode plans: each wave task's items are the chunks of one
+    // (sequence, KV head, row block); the workgroup merges its rows over the
+    // sequence's slots (slot_ptr) into out itself.  0 / null otherwise.
+    uint32_t wave_direct;
+    const uint32_t* slot_ptr;
+    void* out;
 };
 
 // What the CSR planning kernel leaves in the workspace for the attention

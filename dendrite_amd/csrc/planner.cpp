@@ -303,12 +303,41 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         }
     }
 
+    // 3b. Direct plans.  When no segment is shared and no item is a group
+    //     item, each (sequence, KV head, row block) can be one workgroup: its
+    //     pages in at most kWaves equal chunks, one per wave, whose partial
+    //     states the workgroup merges itself, so the step is one launch.
+    //     Taken when the chunks stay short (a sequence of at most
+    //     kWaves * kDirectShortChunk pages: longer ones run faster as more,
+    //     shorter chunks over more waves, merged by the merge kernel) or the
+    //     workgroups alone give the target's worth of waves, each chunk fits
+    //     a wave item's page ids, and every sequence has pages (the merge
+    //     kernel writes the zeros of an empty one).
+    bool direct = false;
+    if (in.direct_ok && !segs.empty()) {
+        constexpr uint32_t kDirectShortChunk = 4;
+        bool ok = true;
+        for (uint32_t b = 0; b < B; ++b) ok = ok && !seq_segs[b].empty();
+        uint32_t max_np = 0;
+        uint64_t blocks = 0;
+        for (const auto& sg : segs) {
+            ok = ok && sg.seqs.size() == 1 && !is_group(sg);
+            max_np = std::max(max_np, uint32_t(sg.pages.size()));
+            blocks += uint64_t(in.hkv) * ceil_div(r, uint32_t(kWaveRows));
+        }
+        ok = ok && ceil_div(max_np, uint32_t(kWaves)) <= uint32_t(kWaveIdRegs) * 64 &&
+             (max_np <= kWaves * kDirectShortChunk || blocks * kWaves >= target);
+        direct = ok;
+    }
+    out.direct = direct;
+
     // 4. Partial-state slots: one per (segment chunk, sequence), contiguous
     //    per sequence.
     std::vector<uint32_t> nchunks(segs.size());
     for (size_t s = 0; s < segs.size(); ++s) {
         const uint32_t ch = is_group(segs[s]) ? group_chunk : wave_chunk;
-        nchunks[s] = ceil_div(uint32_t(segs[s].pages.size()), ch);
+        nchunks[s] = direct ? std::min<uint32_t>(kWaves, uint32_t(segs[s].pages.size()))
+                            : ceil_div(uint32_t(segs[s].pages.size()), ch);
     }
     out.slot_ptr.assign(B + 1, 0);
     for (uint32_t b = 0; b < B; ++b) {
@@ -325,6 +354,7 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     out.tail_n.assign(B, 0);
     out.tail_cap.assign(B, 0);
     std::vector<std::pair<double, Item>> waves;
+    std::vector<std::pair<double, std::vector<Item>>> direct_tasks;
     // Distinct pages of the plan, for the statistics: a bitmap over the pool.
     std::vector<uint64_t> seen((uint64_t(in.num_pool_pages) + 63) / 64, 0);
     uint64_t uniq = 0;
@@ -353,6 +383,36 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         const uint32_t rows = uint32_t(sg.seqs.size()) * r;
         const uint32_t block = grp ? in.group_rows : uint32_t(kWaveRows);
         const uint32_t nrb = ceil_div(rows, block);
+        if (direct) {
+            // One task per (KV head, row block): its chunks, then empty
+            // items up to kWaves (kept in this order by the task packing).
+            const uint32_t seq_off = uint32_t(out.seqslots.size());
+            const uint32_t b = sg.seqs[0];
+            for (uint32_t ci = 0; ci < nc; ++ci) out.seqslots.push_back(SeqSlot{b, cursor[b]++});
+            for (uint32_t h = 0; h < in.hkv; ++h) {
+                for (uint32_t rb = 0; rb < nrb; ++rb) {
+                    double cost = 0.0;
+                    std::vector<Item> task;
+                    for (uint32_t ci = 0; ci < uint32_t(kWaves); ++ci) {
+                        Item it;
+                        const uint32_t p0 = ci < nc ? uint32_t(uint64_t(ci) * np / nc) : np;
+                        const uint32_t p1 = ci < nc ? uint32_t(uint64_t(ci + 1) * np / nc) : np;
+                        it.page_off = base + (ci < nc ? p0 : 0u);
+                        it.npages = p1 - p0;
+                        it.seq_off = seq_off + (ci < nc ? ci : 0u);
+                        it.row_begin = rb * block;
+                        it.nrows = std::min(block, rows - rb * block);
+                        it.kv_head = h;
+                        it.flags = (sg.tail && ci + 1 == nc) ? kItemTail : 0u;
+                        it.tail_seq = sg.tail ? b : 0u;
+                        cost += double(it.npages);
+                        task.push_back(it);
+                    }
+                    direct_tasks.emplace_back(cost, std::move(task));
+                }
+            }
+            continue;
+        }
         for (uint32_t ci = 0; ci < nc; ++ci) {
             const uint32_t p0 = uint32_t(uint64_t(ci) * np / nc);
             const uint32_t p1 = uint32_t(uint64_t(ci + 1) * np / nc);
@@ -429,8 +489,15 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         out.tasks.push_back(Task{kTaskWaves, uint32_t(out.items.size()), n, 0u});
         for (uint32_t k = 0; k < n; ++k) out.items.push_back(waves[i + k].second);
     }
+    // Direct tasks, heaviest first; each keeps its kWaves items in order.
+    std::stable_sort(direct_tasks.begin(), direct_tasks.end(),
+                     [](const auto& x, const auto& y) { return x.first > y.first; });
+    for (const auto& dt : direct_tasks) {
+        out.tasks.push_back(Task{kTaskWaves, uint32_t(out.items.size()), uint32_t(kWaves), 0u});
+        for (const Item& it : dt.second) out.items.push_back(it);
+    }
     out.num_group_items = uint32_t(gorder.size());
-    out.num_wave_items = uint32_t(waves.size());
+    out.num_wave_items = uint32_t(waves.size() + direct_tasks.size() * kWaves);
     for (const Item& it : out.items)
         if (it.npages > kMaxItemPages) {
             err = "internal: an item of " + std::to_string(it.npages) + " pages";

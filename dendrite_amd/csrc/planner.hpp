@@ -26,6 +26,7 @@ struct PlanInput {
     uint32_t shared_chunk_pages = 0;    // 0 = default
     uint32_t private_chunk_pages = 0;
     uint32_t target_items = 0;
+    bool direct_ok = true;              // decode: a direct plan where one qualifies
 };
 
 struct HostPlan {
@@ -35,6 +36,10 @@ struct HostPlan {
     std::vector<SeqSlot> seqslots;
     std::vector<uint32_t> slot_ptr;     // [batch + 1]
     uint32_t num_slots = 0;
+    // Direct decode plan: wave task b holds the (at most kWaves) chunks of
+    // one (sequence, KV head, row block), padded with empty items, and its
+    // waves merge their own partial states (no merge kernel).
+    bool direct = false;
     uint32_t num_group_items = 0;
     uint32_t num_wave_items = 0;
     uint32_t num_segments = 0;

@@ -217,8 +217,18 @@ typedef struct dh_plan_options {
     uint32_t shared_chunk_pages;   /* max pages of a shared segment per item   */
     uint32_t private_chunk_pages;  /* max pages of a private tail per item     */
     uint32_t target_items;         /* split chunks until about this many items */
-    uint32_t reserved[5];
+    uint32_t direct;               /* DH_DIRECT_AUTO or DH_DIRECT_OFF          */
+    uint32_t reserved[4];
 } dh_plan_options;
+
+/* dh_plan_options.direct: by default a decode plan in which no page run is
+ * shared and every (sequence, KV head, block of 16 query rows) fits one
+ * workgroup (its pages in at most four chunks, one per wave) is "direct":
+ * each workgroup merges its waves' partial states itself and writes out, so
+ * dh_decode_batch is one kernel launch.  DH_DIRECT_OFF plans it like any
+ * other (chunks merged by the merge kernel). */
+#define DH_DIRECT_AUTO 0u
+#define DH_DIRECT_OFF 1u
 
 /* Build the work decomposition of one decode step from host-side page lists
  * in CSR form (indices[indptr[b] .. indptr[b+1]) are sequence b's pages in
@@ -280,6 +290,7 @@ typedef struct dh_plan_stats {
     uint32_t num_tasks;           /* workgroups of the attention launch       */
     uint32_t num_group_items;     /* items whose pages four waves share       */
     uint32_t num_partials;        /* partial states per q head                */
+    uint32_t direct;              /* 1: no merge launch (dh_plan_options.direct) */
     uint64_t unique_pages;        /* distinct pages read per step             */
     uint64_t page_reads;          /* pages read per step summed over items of
                                      one kv head (== unique_pages when every

@@ -149,6 +149,41 @@ def test_scores_rising_late(backend, shape, fmt):
     assert np.all(np.isfinite(got)), "non-finite output"
     assert err <= TOL[w.q_dtype], err
 
+
+@pytest.mark.parametrize("fmt", FORMATS + FORMATS_F16Q,
+                         ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8", "f16q-mxfp8"])
+@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256), (16, 1, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_direct_plans(backend, fmt, shape):
+    """Flat plans of short sequences run direct (each (sequence, KV head,
+    row block) one workgroup whose waves merge their own states, no merge
+    launch): against the oracle, and against the same plan with the merge
+    kernel (DIRECT_OFF).  (16, 1, 64) fills the 16-row block; sequences of
+    1-3 pages leave some waves of their workgroup with empty items.  (More
+    than 16 query heads per KV head make group items: never direct.)"""
+    hq, hkv, d = shape
+    tables, nxt = [], 1
+    for b in range(7):
+        n = [1, 2, 3, 5, 16, 11, 9][b]
+        tables.append(list(range(nxt, nxt + n)))
+        nxt += n
+    w = workloads.custom(tables, hq, hkv, d, fmt[0], fmt[1], nxt + 1,
+                         last_page_len=[1, 16, 7, 3, 12, 16, 5], name="direct")
+    run, _ = _check(w, backend, cascade=False)
+    assert run.plan.stats()["direct"] == 1
+    off, _ = _check(w, backend, cascade=False, direct=False)
+    assert off.plan.stats()["direct"] == 0
+    got, ref = run.run(), off.run()
+    assert np.max(np.abs(got - ref)) <= 2 * TOL[w.q_dtype] + 2.0 ** -6
+
+
+def test_c3_flat_runs_direct(backend):
+    """C3's leaves as a flat batch (no cascade): 64 x 8 workgroups of four
+    134-page chunks each fill the chip, so the plan is direct; all 64 leaves
+    against the oracle."""
+    run, _ = _check(workloads.c3(), backend, cascade=False)
+    assert run.plan.stats()["direct"] == 1
+
 def test_empty_sequences(backend):
     """Sequences without pages get zeros (backend.rs:218-222), also when no
     sequence of the batch has a page (no attention item at all)."""

@@ -34,9 +34,17 @@ def _check_cover(w, plan):
     got = {}                       # (b, kv head, j) -> Counter of pages
     written = Counter()            # (slot, kv head, j)
     slot_owner = {}
-    for it in plan["items"]:
+    items = plan["items"]
+    for k, it in enumerate(items):
         pl = pages[it["page_off"]:it["page_off"] + it["npages"]]
-        assert it["npages"] >= 1
+        if it["npages"] == 0:
+            # Only direct plans pad a workgroup's four wave items with empty
+            # ones, after the chunks, rows equal to the task's first item.
+            assert plan["stats"]["direct"] == 1
+            first = items[k - k % 4]
+            assert first["npages"] >= 1 and (it["row_begin"], it["nrows"], it["kv_head"]) == \
+                (first["row_begin"], first["nrows"], first["kv_head"])
+            continue
         for rho in range(it["row_begin"], it["row_begin"] + it["nrows"]):
             b, slot = (int(x) for x in seqslots[it["seq_off"] + rho // r])
             j = rho % r
@@ -172,3 +180,22 @@ def test_sequence_length_limit():
     with pytest.raises(DhError) as e:
         plan_inspect(cfg, n + 1, np.array([0, n + 1], np.uint32), np.arange(n + 1, dtype=np.uint32))
     assert e.value.status == _lib.DH_EINVAL
+
+
+def test_direct_plan_selection():
+    """Direct (merge-free) decode plans: flat plans of short sequences, or
+    whose (sequence, KV head) workgroups alone fill the target; never with a
+    shared segment, a group item, an empty sequence or DIRECT_OFF."""
+    def direct(w, cascade=True, **kw):
+        return plan_inspect(_cfg(w), w.num_pool_pages, w.indptr, w.indices, cascade=cascade, **kw)["stats"]["direct"]
+    short = workloads.custom([[1, 2], [3], [4, 5, 6, 7]], 32, 8, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 16)
+    assert direct(short) == 1
+    assert direct(short, direct=False) == 0
+    assert direct(workloads.c1()) == 0                 # 32 pages: more, shorter chunks do better
+    assert direct(workloads.c3(), cascade=False) == 1  # 64 x 8 workgroups fill the chip
+    assert direct(workloads.c3()) == 0                 # shared prefixes
+    assert direct(workloads.c4()) == 0                 # forked sequences share pages
+    empty = workloads.custom([[1, 2], [], [3]], 32, 8, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 16)
+    assert direct(empty) == 0
+    many_heads = workloads.custom([[1, 2], [3]], 64, 2, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 16)
+    assert direct(many_heads) == 0                     # 32 query heads per KV head: group items
