@@ -2021,7 +2021,7 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
 
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
-template <int D, uint32_t OUT>
+template <int D, uint32_t OUT, int U = 16>
 __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
                                           uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane);
 
@@ -2241,12 +2241,12 @@ __device__ __forceinline__ void load_partial(const void* ws, uint64_t e, float (
 }
 
 // One wave merges output row (b, qh) over partial slots s0 .. s0 + n - 1
-// (no slot: zeros).
-template <int D, uint32_t OUT>
+// (no slot: zeros).  U partial rows are loaded per pass: a row with at
+// most U states costs one round trip after its slot range.
+template <int D, uint32_t OUT, int U>
 __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
                                           uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane) {
     constexpr int PL = D / 64;
-    constexpr int U = 16;
     float acc[PL];
     #pragma unroll
     for (int k = 0; k < PL; ++k) acc[k] = 0.f;
@@ -2323,7 +2323,7 @@ __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws
     }
 }
 
-template <int D, uint32_t OUT>
+template <int D, uint32_t OUT, int U>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -2337,7 +2337,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
     const uint32_t s0 = a.slot_ptr[b];
     const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
-    merge_row<D, OUT>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
+    merge_row<D, OUT, U>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
 }
 
 // ------------------------------------------------- decode from device CSR
@@ -2543,9 +2543,16 @@ hipError_t launch_merge_d(const MergeArgs& a, uint32_t q_dtype, hipStream_t s) {
     const uint32_t rows = a.batch * a.hq;
     if (rows == 0) return hipSuccess;
     dim3 grid((rows + 3) / 4), block(256);
-    if (q_dtype == 2) hipLaunchKernelGGL((merge_kernel<D, 2>), grid, block, 0, s, a);
-    else if (q_dtype == 1) hipLaunchKernelGGL((merge_kernel<D, 1>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((merge_kernel<D, 0>), grid, block, 0, s, a);
+    // Rows of more than 16 states load 32 per pass (one pass up to 32).
+    if (a.wide) {
+        if (q_dtype == 2) hipLaunchKernelGGL((merge_kernel<D, 2, 32>), grid, block, 0, s, a);
+        else if (q_dtype == 1) hipLaunchKernelGGL((merge_kernel<D, 1, 32>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((merge_kernel<D, 0, 32>), grid, block, 0, s, a);
+    } else {
+        if (q_dtype == 2) hipLaunchKernelGGL((merge_kernel<D, 2, 16>), grid, block, 0, s, a);
+        else if (q_dtype == 1) hipLaunchKernelGGL((merge_kernel<D, 1, 16>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((merge_kernel<D, 0, 16>), grid, block, 0, s, a);
+    }
     return hipGetLastError();
 }
 
