@@ -283,8 +283,11 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
         }
         return n;
     };
-    while (count_waves(group_chunk, wave_chunk) < target && (group_chunk > 8 || wave_chunk > 4)) {
-        if (wave_chunk > 4) wave_chunk /= 2;
+    // Below the target, chunks halve down to one page for wave items (C1,
+    // one 32-page sequence: 4-page chunks 10.6 us a step, 1-page chunks 8.0)
+    // and eight pages for group items.
+    while (count_waves(group_chunk, wave_chunk) < target && (group_chunk > 8 || wave_chunk > 1)) {
+        if (wave_chunk > 1) wave_chunk /= 2;
         if (count_waves(group_chunk, wave_chunk) >= target) break;
         if (group_chunk > 8) group_chunk /= 2;
     }
