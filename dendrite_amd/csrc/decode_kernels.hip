@@ -306,8 +306,11 @@ __device__ __forceinline__ void write_wave_partial(const AttendArgs& a, const It
 }
 
 // Query rows of NRT tiles as B operands: lane (g, c) holds row row0+16*rt+c,
-// dims kb*32 + 8g .. +8 (zero for rows outside the item).
-template <int D, int RT>
+// dims kb*32 + 8g .. +8 (zero for rows outside the item).  K16: the order
+// of 8-bit K rows loaded in 16-byte pieces (load_page_k): k-block kb = 2j + h
+// holds dims 64j + 16g + 8h .. +8.  A dot product does not depend on the
+// order of its terms, so K and q only have to agree on it.
+template <int D, int RT, bool K16 = false>
 __device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, uint32_t row0, int nrt,
                                          uint32_t (&qB)[RT][D / 32][4], uint32_t (&dst)[RT], int g, int c) {
     constexpr int KB = D / 32;
@@ -322,7 +325,7 @@ __device__ __forceinline__ void load_q16(const AttendArgs& a, const Item& it, ui
             const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (uint64_t(seq) * a.hq + qh) * D;
             #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                load_dwords<4>(qB[rt][kb], qp + kb * 32 + 8 * g);
+                load_dwords<4>(qB[rt][kb], qp + (K16 ? 64 * (kb >> 1) + 16 * g + 8 * (kb & 1) : kb * 32 + 8 * g));
                 #pragma unroll
                 for (int i = 0; i < 4; ++i) qB[rt][kb][i] ^= a.q_sign;
             }
@@ -487,14 +490,31 @@ __device__ __forceinline__ void load_page_k(PageRaw<D, KVF>& r, const AttendArgs
     using R = PageRaw<D, KVF>;
     constexpr int EB = R::FP8 ? 1 : 2;
     const uint8_t* kp = a.kv + plane_offset(page, 0, head, a.hkv, D, EB);
-    #pragma unroll
-    for (int kb = 0; kb < R::KB; ++kb)
-        load_dwords<R::KW>(r.k[kb], kp + (c * D + kb * 32 + 8 * g) * EB);
+    if constexpr (R::FP8) {
+        // 16 codes (16 bytes) per lane: dims 64j + 16g .. +16 of token c
+        // feed k-blocks 2j and 2j + 1 (the query is loaded in the same
+        // order), so a load instruction reads 64-byte runs of 16 rows
+        // instead of 32-byte ones.
+        #pragma unroll
+        for (int j = 0; j < R::KB / 2; ++j) {
+            uint32_t t[4];
+            load_dwords<4>(t, kp + c * D + 64 * j + 16 * g);
+            r.k[2 * j][0] = t[0];
+            r.k[2 * j][1] = t[1];
+            r.k[2 * j + 1][0] = t[2];
+            r.k[2 * j + 1][1] = t[3];
+        }
+    } else {
+        #pragma unroll
+        for (int kb = 0; kb < R::KB; ++kb)
+            load_dwords<R::KW>(r.k[kb], kp + (c * D + kb * 32 + 8 * g) * EB);
+    }
     if constexpr (KVF == KVF_MX) {
+        // the MX group (32 dims) of k-block 2j + h's codes is 2j + g / 2
         const uint8_t* s = reinterpret_cast<const uint8_t*>(a.scales) +
                            ((uint64_t(page) * 2 + 0) * a.hkv + head) * uint64_t(kPageSize) * R::G;
         #pragma unroll
-        for (int kb = 0; kb < R::G; ++kb) r.ksc[kb] = s[c * R::G + kb];
+        for (int kb = 0; kb < R::G; ++kb) r.ksc[kb] = s[c * R::G + 2 * (kb >> 1) + (g >> 1)];
     }
 }
 
@@ -569,7 +589,7 @@ __device__ __forceinline__ void wave_item(const AttendArgs& a, const Item& it, i
     constexpr bool BLOCK_SCALE = (KVF == KVF_FP8);
     uint32_t qB[1][KB][4];
     uint32_t dst[1];
-    load_q16<D, 1>(a, it, 0, 1, qB, dst, g, c);
+    load_q16<D, 1, PageRaw<D, KVF>::FP8>(a, it, 0, 1, qB, dst, g, c);
     float m[1] = {kNegInf};
     f4 L[1] = {f4{0.f, 0.f, 0.f, 0.f}};
     f4 O[1][EPL];
