@@ -1941,7 +1941,10 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
             constexpr uint32_t j = decltype(J)::value;
             const uint32_t pi = p0 + j;
             if (pi >= nmain) return;
-            wait_vmcnt_any((min(pi + P - 1, npairs) - pi - 2) * C8::PER_PAIR);   // raw pair pi + 1
+            // raw pair pi + 1 has landed: an immediate count while pairs
+            // are still being issued (a runtime count is a tree of branches)
+            if (pi + P - 1 <= npairs) wait_vmcnt_const<(P - 3) * C8::PER_PAIR>();
+            else wait_vmcnt_any((npairs - pi - 2) * C8::PER_PAIR);
             block_barrier();
             if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
             nid0 = page_id(2 * (pi + P));
