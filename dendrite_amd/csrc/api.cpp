@@ -911,9 +911,7 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
         m.out = out;
         m.batch = pl->batch;
         m.hq = c.num_heads;
-        // 17-32 states: one pass of 32 loads (C3, 19: -0.65 µs a step); above
-        // 32, passes of 16 measured faster (C2, 36: -0.65 µs).
-        m.wide = pl->max_slots > 16 && pl->max_slots <= 32 ? 1u : 0u;
+        m.max_states = pl->max_slots;
         hipError_t e = hipError_t(dh::launch_merge(m, c.q_dtype, c.head_dim, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
     }
@@ -1095,7 +1093,7 @@ dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_confi
     m.seq_bad = seq_bad;
     m.csr_hdr = hdr;
     m.status = status;
-    m.wide = 1u;   // chunks per sequence are chosen on the device
+    m.max_states = 0;   // chunks per sequence are chosen on the device
     e = hipError_t(dh::launch_merge(m, c.q_dtype, c.head_dim, stream));
     if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
     return DH_OK;

@@ -37,6 +37,7 @@
 // (exact: power-of-two scaling).
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <type_traits>
 #include "dh_device.hpp"
 #include "dendrite_hip.h"
 
@@ -2044,7 +2045,24 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
 
 // ---------------------------------------------------------------- attend16
 // q in bf16 (KV bf16 / FP8 E4M3 / MXFP8) or f16 (KV f16); bf16/f16 MFMA.
-template <int D, uint32_t OUT, int U = 16>
+// Partial-row layout seen by the merge: a lane loads 16 bytes of a state row.
+template <int D, uint32_t OUT>
+struct MergeShape {
+    static constexpr int ES = OUT == 2 ? 4 : 2;      // bytes per partial element (f32 or scaled f16)
+    static constexpr int EPL = 16 / ES;              // elements per lane per load
+    static constexpr int LPS = D / EPL;              // lanes per state row
+    static constexpr int SPI = 64 / LPS;             // states per load instruction
+    static constexpr int MAX_NV = 64 / SPI < 16 ? 64 / SPI : 16;
+    static_assert(LPS >= 1 && LPS <= 64 && 64 % LPS == 0, "head_dim");
+    // loads per pass for rows of at most `states` states (a power of two)
+    static constexpr int nv_for(int states) {
+        int need = (states + SPI - 1) / SPI, nv = 1;
+        while (nv < need && nv < MAX_NV) nv *= 2;
+        return nv;
+    }
+};
+
+template <int D, uint32_t OUT, int NV>
 __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
                                           uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane);
 
@@ -2066,7 +2084,8 @@ __device__ __forceinline__ void wave_task_merge(const AttendArgs& a, int wave, i
         qh = __builtin_amdgcn_readfirstlane(qh);
         const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.slot_ptr[seq]);
         const uint32_t n = __builtin_amdgcn_readfirstlane(a.slot_ptr[seq + 1]) - s0;
-        merge_row<D, OUT>(a.ws_o, a.ws_lse, a.out, a.hq, seq, qh, s0, n, lane);
+        // at most kWaves states per row
+        merge_row<D, OUT, MergeShape<D, OUT>::nv_for(kWaves)>(a.ws_o, a.ws_lse, a.out, a.hq, seq, qh, s0, n, lane);
     }
 }
 
@@ -2263,12 +2282,102 @@ __device__ __forceinline__ void load_partial(const void* ws, uint64_t e, float (
     }
 }
 
+// merge_row for at most 64 states: a lane loads 16 bytes of one state row
+// (LPS lanes cover a row, so one load instruction reads SPI = 64 / LPS
+// states), all of a pass's loads are issued together with the
+// log-sum-exps, and the SPI lane groups' weighted sums are added across
+// lanes at the end.  One pass covers NV * SPI states (NV chosen for the
+// plan's most states per row), so such a row costs one memory round trip
+// after its slot range.
+template <int D, uint32_t OUT, int NV>
+__device__ __forceinline__ void merge_row_v(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
+                                            uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane) {
+    using MS = MergeShape<D, OUT>;
+    constexpr int ES = MS::ES, EPL = MS::EPL, LPS = MS::LPS, SPI = MS::SPI;
+    static_assert(NV >= 1 && NV <= MS::MAX_NV, "loads per pass");
+    const int grp = lane / LPS, e = lane % LPS;
+    float acc[EPL];
+    #pragma unroll
+    for (int i = 0; i < EPL; ++i) acc[i] = 0.f;
+    float W = 0.f;
+    if (n != 0) {
+        const PartialLse pk = uint32_t(lane) < n ? ws_lse[uint64_t(s0 + lane) * hq + qh]
+                                                 : PartialLse{kNegInf, 0.f};
+        const uint8_t* base = static_cast<const uint8_t*>(ws_o) + (uint64_t(s0) * hq + qh) * (D * ES) + 16 * e;
+        const uint64_t sstride = uint64_t(hq) * (D * ES);
+        u32x4 v[NV];
+        auto load = [&](uint32_t j0) {
+            #pragma unroll
+            for (int u = 0; u < NV; ++u) {
+                const uint32_t st = min(j0 + uint32_t(u * SPI + grp), n - 1);
+                v[u] = *reinterpret_cast<const u32x4*>(base + st * sstride);
+            }
+        };
+        load(0);
+        const float M = wave_max(pk.lse);
+        if (M != kNegInf) {
+            const float wk = pk.lse == kNegInf ? 0.f : fast_exp2(pk.lse - M);
+            W = wk;
+            const float wo = __builtin_amdgcn_ldexpf(wk, int(pk.k));   // weight of the stored (scaled) O
+            for (uint32_t j0 = 0; j0 < n; j0 += NV * SPI) {
+                if (j0) load(j0);
+                #pragma unroll
+                for (int u = 0; u < NV; ++u) {
+                    const uint32_t st = j0 + uint32_t(u * SPI + grp);
+                    const float w = __shfl(wo, int(st & 63u), 64);
+                    const float wu = st < n ? w : 0.f;
+                    if constexpr (OUT == 2) {
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[i] += wu * __uint_as_float(v[u][i]);
+                    } else {
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            acc[2 * i] += wu * unpack_lo(v[u][i], true);
+                            acc[2 * i + 1] += wu * unpack_hi(v[u][i], true);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    #pragma unroll
+    for (int o = LPS; o < 64; o <<= 1)
+        #pragma unroll
+        for (int i = 0; i < EPL; ++i) acc[i] += __shfl_xor(acc[i], o, 64);
+    W = wave_sum(W);
+    const float inv = W > 0.f ? 1.f / W : 0.f;
+    if (lane < LPS) {
+        uint8_t* o = static_cast<uint8_t*>(out) + ((uint64_t(b) * hq + qh) * D + e * EPL) * (OUT == 2 ? 4 : 2);
+        if constexpr (OUT == 2) {
+            *reinterpret_cast<f4*>(o) = f4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        } else {
+            u32x4 w;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = pack2(acc[2 * i] * inv, acc[2 * i + 1] * inv, OUT == 0);
+            *reinterpret_cast<u32x4*>(o) = w;
+        }
+    }
+}
+
 // One wave merges output row (b, qh) over partial slots s0 .. s0 + n - 1
-// (no slot: zeros).  U partial rows are loaded per pass: a row with at
-// most U states costs one round trip after its slot range.
-template <int D, uint32_t OUT, int U>
+// (no slot: zeros).  NV > 0: rows of up to 64 states take merge_row_v.
+// Otherwise (NV = 0, and rows of more than 64 states) a lane loads 4-8 bytes
+// of every state row, U partial rows per pass (32 for NV = 0, else 16): a
+// row of at most U states costs one round trip after its slot range.  On
+// MI355X the vector form is faster for 36 states at head_dim 64 (C2, one
+// pass instead of two: 10.5 -> 9.6 us a step), the same for 2-9 (C1, C4,
+// C5), and slower for 19 at head_dim 128 (C3: 28.0 against 27.6), which
+// keeps the scalar form.
+template <int D, uint32_t OUT, int NV>
 __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws_lse, void* out, uint32_t hq,
                                           uint32_t b, uint32_t qh, uint32_t s0, uint32_t n, int lane) {
+    if constexpr (NV > 0) {
+        if (n <= 64) {
+            merge_row_v<D, OUT, NV>(ws_o, ws_lse, out, hq, b, qh, s0, n, lane);
+            return;
+        }
+    }
+    constexpr int U = NV == 0 ? 32 : 16;
     constexpr int PL = D / 64;
     float acc[PL];
     #pragma unroll
@@ -2346,7 +2455,7 @@ __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws
     }
 }
 
-template <int D, uint32_t OUT, int U>
+template <int D, uint32_t OUT, int NV>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -2360,7 +2469,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
     const uint32_t s0 = a.slot_ptr[b];
     const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
-    merge_row<D, OUT, U>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
+    merge_row<D, OUT, NV>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
 }
 
 // ------------------------------------------------- decode from device CSR
@@ -2566,16 +2675,24 @@ hipError_t launch_merge_d(const MergeArgs& a, uint32_t q_dtype, hipStream_t s) {
     const uint32_t rows = a.batch * a.hq;
     if (rows == 0) return hipSuccess;
     dim3 grid((rows + 3) / 4), block(256);
-    // Rows of more than 16 states load 32 per pass (one pass up to 32).
-    if (a.wide) {
-        if (q_dtype == 2) hipLaunchKernelGGL((merge_kernel<D, 2, 32>), grid, block, 0, s, a);
-        else if (q_dtype == 1) hipLaunchKernelGGL((merge_kernel<D, 1, 32>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((merge_kernel<D, 0, 32>), grid, block, 0, s, a);
-    } else {
-        if (q_dtype == 2) hipLaunchKernelGGL((merge_kernel<D, 2, 16>), grid, block, 0, s, a);
-        else if (q_dtype == 1) hipLaunchKernelGGL((merge_kernel<D, 1, 16>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((merge_kernel<D, 0, 16>), grid, block, 0, s, a);
-    }
+    // Rows of 17-32 states: the scalar form, one pass of 32.  Otherwise the
+    // vector form with loads per pass for the plan's most states per row (0:
+    // not known on the host, up to 64), so a row loads no state twice.
+    const int states = a.max_states == 0 || a.max_states > 64 ? 64 : int(a.max_states);
+    auto go = [&](auto out_tag) {
+        constexpr uint32_t OUT = decltype(out_tag)::value;
+        using MS = MergeShape<D, OUT>;
+        const int need = (states + MS::SPI - 1) / MS::SPI;
+        if (states > 16 && states <= 32) hipLaunchKernelGGL((merge_kernel<D, OUT, 0>), grid, block, 0, s, a);
+        else if (need <= 1) hipLaunchKernelGGL((merge_kernel<D, OUT, 1>), grid, block, 0, s, a);
+        else if (need <= 2 && MS::MAX_NV >= 2) hipLaunchKernelGGL((merge_kernel<D, OUT, (MS::MAX_NV >= 2 ? 2 : 1)>), grid, block, 0, s, a);
+        else if (need <= 4 && MS::MAX_NV >= 4) hipLaunchKernelGGL((merge_kernel<D, OUT, (MS::MAX_NV >= 4 ? 4 : 1)>), grid, block, 0, s, a);
+        else if (need <= 8 && MS::MAX_NV >= 8) hipLaunchKernelGGL((merge_kernel<D, OUT, (MS::MAX_NV >= 8 ? 8 : 1)>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((merge_kernel<D, OUT, MS::MAX_NV>), grid, block, 0, s, a);
+    };
+    if (q_dtype == 2) go(std::integral_constant<uint32_t, 2>{});
+    else if (q_dtype == 1) go(std::integral_constant<uint32_t, 1>{});
+    else go(std::integral_constant<uint32_t, 0>{});
     return hipGetLastError();
 }
 

@@ -161,7 +161,7 @@ struct MergeArgs {
     const PartialLse* ws_lse;
     void* out;                   // [B][Hq][D]
     uint32_t batch, hq;
-    uint32_t wide;               // 1: rows load 32 partial states per pass (else 16)
+    uint32_t max_states;         // most partial states of a row (0: not known, up to 64)
     // CSR path (null otherwise): sequences marked bad get zeros, and the
     // call's status (DH_OK / DH_EINVAL / DH_ENOMEM) goes to *status.
     const uint32_t* seq_bad;
