@@ -313,8 +313,16 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     //    group items of up to in.group_rows rows whose four waves share every
     //    page through LDS.  Chunks split a segment's pages over items: more
     //    chunks give more parallelism and more partial states.
+    // A short segment of a few row blocks (at most 4 x 16 rows and 16 pages)
+    // stays wave items: a group item's start (row targets, query rows and
+    // first pairs, three dependent round trips) costs more than reading its
+    // pages once per row block, mostly from L2.  C3 (whose level-1 nodes are
+    // 8 pages under 64 rows), six rotations: 27.7 -> 26.8-27.5 us a step;
+    // 16-page levels 42.0 -> 41.6 us.
     auto is_group = [&](const Segment& sg) {
-        return !in.wave_items_only && uint32_t(sg.seqs.size()) * r > uint32_t(kWaveRows);
+        const uint32_t rows = uint32_t(sg.seqs.size()) * r;
+        if (in.wave_items_only || rows <= uint32_t(kWaveRows)) return false;
+        return rows > 4u * kWaveRows || sg.pages.size() > 16;
     };
     uint32_t group_chunk = std::min<uint32_t>(in.shared_chunk_pages ? in.shared_chunk_pages : 32,
                                               kGroupMaxPages);

@@ -152,15 +152,18 @@ def test_scores_rising_late(backend, shape, fmt):
 
 @pytest.mark.parametrize("fmt", FORMATS + FORMATS_F16Q,
                          ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8", "f16q-mxfp8"])
-@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256), (16, 1, 64)],
+@pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256), (16, 1, 64), (64, 2, 128),
+                                   (32, 1, 64)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_direct_plans(backend, fmt, shape):
     """Flat plans of short sequences run direct (each (sequence, KV head,
     row block) one workgroup whose waves merge their own states, no merge
     launch): against the oracle, and against the same plan with the merge
-    kernel (DIRECT_OFF).  (16, 1, 64) fills the 16-row block; sequences of
-    1-3 pages leave some waves of their workgroup with empty items.  (More
-    than 16 query heads per KV head make group items: never direct.)"""
+    kernel (DIRECT_OFF).  (16, 1, 64) fills the 16-row block; (64, 2, 128)
+    and (32, 1, 64) give each (sequence, KV head) two row blocks, two
+    workgroups; sequences of 1-3 pages leave some waves of their workgroup
+    with empty items.  (Runs of more than 16 pages under more than 16 rows,
+    or more than 64 rows, make group items: never direct.)"""
     hq, hkv, d = shape
     tables, nxt = [], 1
     for b in range(7):

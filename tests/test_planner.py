@@ -197,5 +197,9 @@ def test_direct_plan_selection():
     assert direct(workloads.c4()) == 0                 # forked sequences share pages
     empty = workloads.custom([[1, 2], [], [3]], 32, 8, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 16)
     assert direct(empty) == 0
+    # 32 query heads per KV head: runs of at most 16 pages stay wave items
+    # (two row blocks), longer ones are group items
     many_heads = workloads.custom([[1, 2], [3]], 64, 2, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 16)
-    assert direct(many_heads) == 0                     # 32 query heads per KV head: group items
+    assert direct(many_heads) == 1
+    long_many_heads = workloads.custom([list(range(1, 21)), [21]], 64, 2, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 32)
+    assert direct(long_many_heads) == 0
