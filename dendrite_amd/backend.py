@@ -182,8 +182,8 @@ class Pool:
         """Quantise-on-write from device tensors: page_ids (uint32 / int32,
         [n]) receive src ([n, 2, num_kv_heads, 16, head_dim] float32 /
         bfloat16 / float16, K then V, zero past a partial page's tokens) in
-        the pool's format (dh_pool_write_pages_device).  Ids outside the pool
-        are skipped."""
+        the pool's format (dh_pool_write_pages_device), on `stream` (default:
+        torch's current stream).  Ids outside the pool are skipped."""
         torch = _torch()
         dtype = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
                  torch.float16: _lib.DTYPE_F16}.get(src.dtype)
@@ -197,8 +197,7 @@ class Pool:
         if page_ids.dtype not in (torch.int32, torch.uint32):
             raise DhError(_lib.DH_EINVAL, "page_ids must be int32 or uint32")
         check(lib().dh_pool_write_pages_device(self._h, C.c_void_p(page_ids.data_ptr()), page_ids.numel(),
-                                               C.c_void_p(src.data_ptr()), dtype,
-                                               _stream_ptr(stream) if stream is not None else None))
+                                               C.c_void_p(src.data_ptr()), dtype, _stream_ptr(stream)))
 
     def write_tokens(self, page_id: int, tok_offset: int, k: np.ndarray, v: np.ndarray,
                      k_scale=None, v_scale=None, stream=None) -> None:
@@ -707,8 +706,9 @@ class HipBackend:
             sh = torch.zeros((1, 2, hkv, _lib.PAGE_SIZE, d), dtype=torch.float32, device=dev)
         sh[0, 0, :, off:off + n] = k.to(dev, torch.float32)
         sh[0, 1, :, off:off + n] = v.to(dev, torch.float32)
+        # On the current stream, after the shadow's updates and before any
+        # later use of it or of the id tensor's memory: no host wait.
         self.pool.write_pages_device(torch.tensor([page], dtype=torch.int32, device=dev), sh)
-        self.backend.synchronize()
         if off + n == _lib.PAGE_SIZE:
             self._shadow.pop(page, None)
         else:

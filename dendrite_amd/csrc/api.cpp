@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -112,6 +113,12 @@ struct dh_pool {
     uint64_t page_bytes, scale_bytes;
     uint8_t* data;
     uint8_t* scales;
+    // Staging memory of host page uploads (dh_pool_write_pages), kept from
+    // call to call and grown when a call needs more; the mutex serialises
+    // uploads that would share it.
+    std::mutex stage_mu;
+    uint8_t* stage = nullptr;
+    uint64_t stage_bytes = 0;
 };
 
 struct dh_plan {
@@ -317,6 +324,7 @@ dh_status dh_pool_destroy(dh_pool* p) {
         (void)hipDeviceSynchronize();
         (void)hipFree(p->data);
         if (p->scales) (void)hipFree(p->scales);
+        if (p->stage) (void)hipFree(p->stage);
         (void)hipGetLastError();
     }
     release(p->be);
@@ -399,10 +407,20 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
     DH_DEVICE(p->be->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint32_t batch = std::min<uint32_t>(n, std::max<uint64_t>(1, (256ull << 20) / p->page_bytes));
-    uint8_t* stage = nullptr;
-    uint32_t* dids = nullptr;
-    DH_HIP(hipMalloc(&stage, batch * (p->page_bytes + p->scale_bytes)));
-    hipError_t e = hipMalloc(&dids, batch * sizeof(uint32_t));
+    std::lock_guard<std::mutex> lock(p->stage_mu);
+    // page data, scale records, page ids: one staging allocation
+    const uint64_t ids_off = (uint64_t(batch) * (p->page_bytes + p->scale_bytes) + 255) & ~uint64_t(255);
+    const uint64_t need = ids_off + uint64_t(batch) * sizeof(uint32_t);
+    if (p->stage_bytes < need) {
+        if (p->stage) (void)hipFree(p->stage);
+        p->stage = nullptr;
+        p->stage_bytes = 0;
+        DH_HIP(hipMalloc(&p->stage, need));
+        p->stage_bytes = need;
+    }
+    uint8_t* stage = p->stage;
+    uint32_t* dids = reinterpret_cast<uint32_t*>(stage + ids_off);
+    hipError_t e = hipSuccess;
     dh_status st = DH_OK;
     for (uint32_t i0 = 0; e == hipSuccess && i0 < n; i0 += batch) {
         const uint32_t m = std::min(batch, n - i0);
@@ -421,8 +439,6 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
         if (e == hipSuccess) e = hipStreamSynchronize(s);
     }
     if (e != hipSuccess) st = fail(DH_EHIP, "page upload failed: %s", hipGetErrorString(e));
-    (void)hipFree(stage);
-    if (dids) (void)hipFree(dids);
     return st;
 }
 
