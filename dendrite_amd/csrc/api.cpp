@@ -152,6 +152,7 @@ struct dh_plan {
     // and there is no merge launch.
     bool direct;
     uint32_t max_slots;      // most partial states of one sequence
+    uint32_t uniform_slots;  // every sequence's count of partial states when they are all equal, else 0
 };
 
 extern "C" {
@@ -633,6 +634,9 @@ static dh_status upload_plan(dh_backend* be, const dh_attn_config* cfg, const dh
     pl->direct = prefill || hp.direct;
     pl->max_slots = 0;
     for (uint32_t v = 0; v < batch; ++v) pl->max_slots = std::max(pl->max_slots, hp.slot_ptr[v + 1] - hp.slot_ptr[v]);
+    pl->uniform_slots = batch ? pl->max_slots : 0;
+    for (uint32_t v = 0; v < batch; ++v)
+        if (hp.slot_ptr[v + 1] - hp.slot_ptr[v] != pl->max_slots) pl->uniform_slots = 0;
     for (uint32_t v = 0; prefill && v < batch; ++v)
         if (hp.slot_ptr[v + 1] - hp.slot_ptr[v] != 1) pl->direct = false;
     pl->items_word = o_items / sizeof(uint32_t);
@@ -928,6 +932,7 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
         m.batch = pl->batch;
         m.hq = c.num_heads;
         m.max_states = pl->max_slots;
+        m.uniform_slots = pl->uniform_slots;
         hipError_t e = hipError_t(dh::launch_merge(m, c.q_dtype, c.head_dim, stream));
         if (e != hipSuccess) return fail(DH_EHIP, "merge launch failed: %s", hipGetErrorString(e));
     }

@@ -2467,8 +2467,11 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     }
     if (row >= a.batch * a.hq) return;
     const uint32_t b = row / a.hq, qh = row - b * a.hq;
-    const uint32_t s0 = a.slot_ptr[b];
-    const uint32_t n = (a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0;
+    // Plans whose sequences all have n slots: the slot range is b*n .. +n,
+    // one dependent load fewer before the partial states.
+    const uint32_t s0 = a.uniform_slots ? b * a.uniform_slots : a.slot_ptr[b];
+    const uint32_t n = a.uniform_slots ? a.uniform_slots
+                                       : ((a.seq_bad && a.seq_bad[b]) ? 0u : a.slot_ptr[b + 1] - s0);
     merge_row<D, OUT, NV>(a.ws_o, a.ws_lse, a.out, a.hq, b, qh, s0, n, lane);
 }
 

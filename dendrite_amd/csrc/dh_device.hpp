@@ -162,6 +162,7 @@ struct MergeArgs {
     void* out;                   // [B][Hq][D]
     uint32_t batch, hq;
     uint32_t max_states;         // most partial states of a row (0: not known, up to 64)
+    uint32_t uniform_slots;      // n > 0: sequence b's slots are b*n .. b*n+n-1 (no slot_ptr read)
     // CSR path (null otherwise): sequences marked bad get zeros, and the
     // call's status (DH_OK / DH_EINVAL / DH_ENOMEM) goes to *status.
     const uint32_t* seq_bad;
