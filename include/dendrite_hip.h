@@ -172,7 +172,10 @@ dh_status dh_pool_write_tokens(dh_pool* pool, uint32_t page_id, uint32_t tok_off
                                uint32_t n_tok, const void* k, const void* v,
                                const void* k_scale, const void* v_scale, void* stream);
 /* Bulk upload of whole pages (data + scale records) from host memory:
- * page_ids[i] receives data[i] and scales[i] in the pool layout above. */
+ * page_ids[i] receives data[i] and scales[i] in the pool layout above.
+ * Returns once the pages are written (the stream is synchronised); the
+ * staging memory is the pool's own, kept from call to call and grown as
+ * needed (uploads into one pool from several threads take turns). */
 dh_status dh_pool_write_pages(dh_pool* pool, const uint32_t* page_ids, uint32_t n,
                               const void* data, const void* scales, void* stream);
 /* Quantise-on-write from device memory: page_ids[i] (device uint32[n]) of
