@@ -180,6 +180,21 @@ def test_direct_plans(backend, fmt, shape):
     assert np.max(np.abs(got - ref)) <= 2 * TOL[w.q_dtype] + 2.0 ** -6
 
 
+@pytest.mark.parametrize("fmt", [FORMATS[0], FORMATS[2]], ids=["bf16", "f32"])
+def test_rows_of_more_than_64_partial_states(backend, fmt):
+    """One-page chunks over 150- and 70-page sequences: rows of 150 and 70
+    partial states, beyond the merge's one-pass form (64), take its
+    multi-pass path; a 40-page sequence in the same plan takes the one-pass
+    form (the plan is not uniform)."""
+    tables, nxt = [], 1
+    for n in (150, 70, 40):
+        tables.append(list(range(nxt, nxt + n)))
+        nxt += n
+    w = workloads.custom(tables, 32, 4, 64, fmt[0], fmt[1], nxt + 1, last_page_len=[5, 16, 9], name="many")
+    run, _ = _check(w, backend, cascade=False, private_chunk_pages=1, direct=False)
+    assert run.plan.stats()["num_partials"] == 260
+
+
 def test_c3_flat_runs_direct(backend):
     """C3's leaves as a flat batch (no cascade): 64 x 8 workgroups of four
     134-page chunks each fill the chip, so the plan is direct; all 64 leaves

@@ -203,3 +203,35 @@ def test_direct_plan_selection():
     assert direct(many_heads) == 1
     long_many_heads = workloads.custom([list(range(1, 21)), [21]], 64, 2, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 32)
     assert direct(long_many_heads) == 0
+
+
+def test_flat_wave_chunk_by_list_schedule():
+    """A plan of wave items only with work to spare takes the wave chunk whose
+    heaviest-first schedule over the chip's wave slots ends first: C4 (256
+    sequences of 32-256 FP8 pages) gets 96-page chunks (measured fastest of
+    32 / 64 / 96 / 128 / 256), and every row still reads its pages once."""
+    w = workloads.c4()
+    plan = plan_inspect(_cfg(w), w.num_pool_pages, w.indptr, w.indices)
+    st = plan["stats"]
+    assert st["num_group_items"] == 0
+    sizes = [int(it["npages"]) for it in plan["items"]]
+    assert max(sizes) == 96 and st["num_items"] == 4120
+    _check_cover(w, plan)
+    # explicit options keep their meaning (no schedule estimate)
+    fixed = plan_inspect(_cfg(w), w.num_pool_pages, w.indptr, w.indices, private_chunk_pages=32)
+    assert max(int(it["npages"]) for it in fixed["items"]) <= 32
+
+
+def test_short_shared_runs_stay_wave_items():
+    """A shared run of at most 16 pages under at most 64 rows is read by wave
+    items, one per 16-row block (C3's level-1 nodes: 8 pages, 16 leaves x 4
+    heads); the 512-page root stays group items of 128 rows."""
+    w = workloads.c3()
+    plan = plan_inspect(_cfg(w), w.num_pool_pages, w.indptr, w.indices)
+    st = plan["stats"]
+    assert st["num_group_items"] == 256                  # root: 16 chunks x 8 heads x 2 row blocks
+    groups = plan["items"][:st["num_group_items"]]
+    assert all(int(it["nrows"]) == 128 and int(it["npages"]) == 32 for it in groups)
+    waves = plan["items"][st["num_group_items"]:]
+    assert max(int(it["nrows"]) for it in waves) == 16
+    _check_cover(w, plan)
