@@ -114,6 +114,22 @@ def measured_traffic(workload: str):
     return t.get("hbm_bytes_per_launch"), f"counters taken at {t.get('commit', '?')[:12]} on these sources"
 
 
+def warm_up(step, args) -> int:
+    """Untimed calls: args.warmup of them, then more until args.warm_seconds
+    of back-to-back calls have run (timed first, the first ~0.1 s of calls
+    run slower than the steady state).  Returns the number of calls."""
+    import torch
+    t0 = time.perf_counter()
+    i = 0
+    while i < args.warmup or time.perf_counter() - t0 < args.warm_seconds:
+        step(i)
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()     # the host clock follows the device
+    torch.cuda.synchronize()
+    return i
+
+
 def bench_prefill(args):
     """Paged causal prefill: B sequences of CTX cached + NEW query tokens in
     shuffled pool pages; q / out [B*NEW, Hq, D] resident in HBM.  The work
@@ -145,9 +161,7 @@ def bench_prefill(args):
     out = torch.empty_like(q)
     ws = plan.workspace()
     stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
-        decode_batch(plan, q, out, ws, stream=stream)
-    torch.cuda.synchronize()
+    warm_up(lambda i: decode_batch(plan, q, out, ws, stream=stream), args)
     res = {}
     for stages in (3, 1):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -349,9 +363,7 @@ def bench_write(args):
     src = torch.randn((n, 2, w.hkv, 16, w.d), generator=g, device="cuda").to(torch.bfloat16)
     ids = torch.randperm(n, device="cuda").to(torch.int32)
     stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
-        pool.write_pages_device(ids, src, stream=stream)
-    torch.cuda.synchronize()
+    warm_up(lambda i: pool.write_pages_device(ids, src, stream=stream), args)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(args.steps):
@@ -470,19 +482,10 @@ def main():
         k = i % R
         decode_batch(plans[k], qs[k], outs[k], ws, lpls[k], stream=stream, stages=stages)
 
-    # Warm-up: the requested steps, then more until --warm-seconds of
-    # back-to-back steps have run.  Timed first, the first ~0.1 s of steps
-    # run slower than the steady state (C5: 898 against 797 us a step, C4 233
-    # against 223), whatever the step count.
+    # Warm-up (warm_up): C5 timed without it 898 against 797 us a step, C4
+    # 233 against 223, whatever the step count.
     t_warm = time.perf_counter()
-    i = 0
-    while i < args.warmup or time.perf_counter() - t_warm < args.warm_seconds:
-        step(i)
-        i += 1
-        if i % 32 == 0:
-            torch.cuda.synchronize()     # the host clock follows the device
-    torch.cuda.synchronize()
-    n_warm = i
+    n_warm = warm_up(step, args)
     log(f"[bench] warm-up: {n_warm} steps in {time.perf_counter() - t_warm:.2f} s")
 
     def timed(stages):
