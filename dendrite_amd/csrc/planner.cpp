@@ -12,8 +12,6 @@
 #include "planner.hpp"
 
 #include <algorithm>
-#include <functional>
-#include <queue>
 #include <unordered_map>
 
 #include "dendrite_hip.h"
@@ -164,29 +162,40 @@ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // step, 64 226, 96 221 (chosen here), 128 235, 256 275.
 uint32_t flat_wave_chunk(const std::vector<Segment>& segs, uint32_t r, uint32_t hkv, uint32_t cur) {
     constexpr uint32_t kSlots = 2048, kStartPairs = 3;
-    constexpr size_t kMaxItems = size_t(1) << 17;   // beyond this, keep cur (planning time)
-    std::vector<uint32_t> cost;
+    std::vector<uint64_t> items;    // items of each cost (in pairs)
+    std::vector<uint64_t> slots;    // slots at each load
+    // Heaviest-first list scheduling, exact, in O(costs + loads): items of
+    // one cost go to the least-loaded slots a level at a time, and the lowest
+    // load only grows.  Loads stay below the mean plus the largest item.
     auto makespan = [&](uint32_t chunk) -> uint64_t {
-        cost.clear();
+        const uint32_t max_cost = kStartPairs + (chunk + 1) / 2;
+        items.assign(max_cost + 1, 0);
+        uint64_t total = 0;
         for (const auto& sg : segs) {
             const uint32_t np = uint32_t(sg.pages.size());
             const uint32_t nc = ceil_div(np, chunk);
-            const uint32_t copies = ceil_div(uint32_t(sg.seqs.size()) * r, uint32_t(kWaveRows)) * hkv;
+            const uint64_t copies = uint64_t(ceil_div(uint32_t(sg.seqs.size()) * r, uint32_t(kWaveRows))) * hkv;
             for (uint32_t ci = 0; ci < nc; ++ci) {
                 const uint32_t n = uint32_t(uint64_t(ci + 1) * np / nc - uint64_t(ci) * np / nc);
-                cost.insert(cost.end(), copies, kStartPairs + (n + 1) / 2);
+                const uint32_t c = kStartPairs + (n + 1) / 2;
+                items[c] += copies;
+                total += copies * c;
             }
-            if (cost.size() > kMaxItems) return 0;
         }
-        std::sort(cost.begin(), cost.end(), std::greater<uint32_t>());
-        std::priority_queue<uint64_t, std::vector<uint64_t>, std::greater<uint64_t>> slots;
-        for (uint32_t k = 0; k < kSlots; ++k) slots.push(0);
-        uint64_t end = 0;
-        for (uint32_t c : cost) {
-            const uint64_t t = slots.top() + c;
-            slots.pop();
-            slots.push(t);
-            end = std::max(end, t);
+        const uint64_t cap = total / kSlots + max_cost + 1;
+        if (cap > (uint64_t(1) << 26)) return 0;
+        slots.assign(cap + 1, 0);
+        slots[0] = kSlots;
+        uint64_t lo = 0, end = 0;
+        for (uint32_t c = max_cost; c >= 1; --c) {
+            for (uint64_t k = items[c]; k != 0;) {
+                while (slots[lo] == 0) ++lo;
+                const uint64_t take = std::min(k, slots[lo]);
+                slots[lo] -= take;
+                slots[lo + c] += take;
+                end = std::max(end, lo + c);
+                k -= take;
+            }
         }
         return end;
     };
