@@ -1,8 +1,8 @@
 """Randomised parity sweep: seeded random fork trees over every head shape and
 dtype / format pair, with random plan options (cascade or flat, chunk sizes,
 direct plans on or off), GQA mappings and softmax scales, through the plan
-path (dh_decode_batch) and the device-CSR path (dh_decode_csr), each case
-against the CPU oracle on the same inputs.  The cases are fixed by the seeds,
+path (dh_decode_batch) and the device-CSR path (dh_decode_csr), and random
+prefill batches, each case against the CPU oracle on the same inputs.  The cases are fixed by the seeds,
 so a failure names a reproducible case (printed before it runs)."""
 import numpy as np
 import pytest
@@ -85,3 +85,28 @@ def test_random_csr_decode(backend, i):
           flush=True)
     assert int(status.item()) == _lib.DH_OK
     assert np.all(np.isfinite(got)) and err <= TOL[w.q_dtype]
+
+
+PREFILL_SHAPES = [(32, 8, 128), (16, 4, 64), (8, 2, 256), (32, 4, 64), (64, 8, 128)]
+PREFILL_FMTS = [(_lib.DTYPE_BF16, _lib.KV_BF16), (_lib.DTYPE_F16, _lib.KV_F16),
+                (_lib.DTYPE_BF16, _lib.KV_FP8_E4M3), (_lib.DTYPE_BF16, _lib.KV_MXFP8)]
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_prefill(backend, i):
+    """Paged prefill: random batches of (context, new tokens), causal or
+    full, chunk sizes, GQA mappings and INVALID ids, against the oracle's
+    decode of each query's virtual sequence (tests/test_gpu_prefill.py)."""
+    from tests.test_gpu_prefill import _run
+    rng = np.random.default_rng([0x9F, i])
+    hq, hkv, d = PREFILL_SHAPES[rng.integers(len(PREFILL_SHAPES))]
+    fmt = PREFILL_FMTS[rng.integers(len(PREFILL_FMTS))]
+    if fmt[1] in (_lib.KV_FP8_E4M3, _lib.KV_MXFP8) and d == 64:
+        d = 128
+    B = int(rng.integers(1, 4))
+    kv = [int(rng.integers(1, 600)) for _ in range(B)]
+    q = [int(rng.integers(1, min(k, 64) + 1)) for k in kv]
+    _run(backend, hq, hkv, d, fmt[0], fmt[1], kv_len=kv, q_len=q, causal=bool(rng.random() < 0.8),
+         chunk_pages=int(rng.choice([0, 0, 1, 3, 8])),
+         gqa=_lib.GQA_INTERLEAVED if rng.random() < 0.3 else _lib.GQA_TILED,
+         invalid=bool(rng.random() < 0.3), seed=int(rng.integers(1 << 20)))
