@@ -439,7 +439,11 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
         }
         if (e == hipSuccess) e = hipStreamSynchronize(s);
     }
-    if (e != hipSuccess) st = fail(DH_EHIP, "page upload failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) {
+        st = fail(DH_EHIP, "page upload failed: %s", hipGetErrorString(e));
+        (void)hipStreamSynchronize(s);   // nothing queued may still use the staging memory
+        (void)hipGetLastError();
+    }
     return st;
 }
 
