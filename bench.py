@@ -381,6 +381,69 @@ def bench_write(args):
                       "steps": args.steps, "warmup": args.warmup}), flush=True)
 
 
+def bench_csr(args):
+    """One decode step through dh_decode_csr (BatchDecodeKernel::run's
+    contract): device int32 CSR tables read on the GPU every call, no plan.
+    The decomposition is flat, so shared pages are streamed once per
+    sequence: the rate is given against the workload's unique bytes (the
+    metric of the planned path) and against the bytes this path reads."""
+    import torch
+    from dendrite_amd import _lib
+    from dendrite_amd.backend import Backend, Pool, csr_workspace_size, decode_csr, raw_to_tensor
+    w = workloads_one(args.workload)
+    be = Backend(0)
+    pool = Pool(be, w.num_pool_pages, w.hkv, w.d, w.kv_format)
+    ids = w.page_ids()
+    for c0 in range(0, len(ids), 8192):
+        data, scales = w.make_pages(ids[c0:c0 + 8192])
+        pool.write_pages(ids[c0:c0 + 8192], data, scales)
+        del data, scales
+    cfg = w.attention_config()
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).cuda()  # noqa: E731
+    ix, ip, lp = dev(w.indices), dev(w.indptr), dev(w.last_page_len)
+    q = raw_to_tensor(w.make_q(), w.q_dtype)
+    out = torch.empty_like(q)
+    ws = torch.empty(csr_workspace_size(cfg, w.batch, int(w.indptr[-1])), dtype=torch.uint8, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        decode_csr(be, pool, cfg, q, ix, ip, lp, out, ws, status, stream=stream)
+
+    warm_up(step, args)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    if int(status.item()) != 0:
+        raise RuntimeError(f"dh_decode_csr status {int(status.item())}")
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    alg = w.algorithmic_bytes()
+    qo = 2 * w.batch * w.hq * w.d * (4 if w.q_dtype == _lib.DTYPE_F32 else 2)
+    streamed = w.naive_kv_bytes() + qo
+    if w.kv_format == _lib.KV_MXFP8:        # one scale byte per 32 values
+        streamed += w.naive_kv_bytes() // 32
+    unique_gbs = alg / (us * 1e-6) / 1e9
+    streamed_gbs = streamed / (us * 1e-6) / 1e9
+    log(f"[bench] csr {w.name}: {us:.2f} us/step, {unique_gbs:.0f} GB/s of unique bytes, "
+        f"{streamed_gbs:.0f} GB/s of streamed bytes")
+    print(json.dumps({"metric": "paged decode step from device CSR (dh_decode_csr)", "value": round(us, 2),
+                      "unit": "us", "higher_is_better": False,
+                      "unique_bytes": alg, "unique_gbs": round(unique_gbs, 1),
+                      "streamed_bytes": streamed, "streamed_gbs": round(streamed_gbs, 1),
+                      "streamed_pct_of_peak_hbm": round(100 * streamed_gbs / PEAK_HBM_GBS, 2),
+                      "config": {"workload": w.name, "batch": w.batch, "num_heads": w.hq,
+                                 "num_kv_heads": w.hkv, "head_dim": w.d, "kv_format": w.kv_format},
+                      "steps": args.steps, "warmup": args.warmup}), flush=True)
+
+
+def workloads_one(name: str):
+    from dendrite_amd import workloads
+    return workloads.ALL[name]()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,6 +470,8 @@ def main():
     ap.add_argument("--write-pages", type=int, default=0, metavar="N",
                     help="only measure quantise-on-write (dh_pool_write_pages_device) of N bf16 pages "
                          "into a pool of the workload's shape and KV format")
+    ap.add_argument("--csr", action="store_true",
+                    help="only measure dh_decode_csr (device CSR tables, no plan) on the workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -442,6 +507,9 @@ def main():
         return
     if args.prefill:
         bench_prefill(args)
+        return
+    if args.csr:
+        bench_csr(args)
         return
 
     ws_list = build_workloads(args.workload, args.rotations)

@@ -1007,9 +1007,11 @@ size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch, uint32_t
     if (!cfg || cfg->num_kv_heads == 0 || cfg->num_heads == 0 || batch == 0) return 0;
     const uint64_t per = uint64_t(cfg->num_kv_heads) * csr_row_blocks(*cfg);
     const uint64_t t = max_total_pages;
+    // Room for chunks that give up to two waves per wave slot, and for the
+    // largest chunks whatever the batch.
     const uint64_t need = (t + dh::kCsrMaxChunk - 1) / dh::kCsrMaxChunk;
     const uint64_t par = std::min((t + dh::kCsrMinChunk - 1) / dh::kCsrMinChunk,
-                                  (uint64_t(dh::kCsrTargetWaves) + per - 1) / per);
+                                  (2 * uint64_t(dh::kCsrWaveSlots) + per - 1) / per);
     const uint64_t extra = std::min(kCsrMaxExtraSlots, std::max<uint64_t>(1, std::max(need, par)));
     return csr_layout(*cfg, batch, uint64_t(batch) + extra).total;
 }

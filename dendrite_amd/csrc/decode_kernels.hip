@@ -188,14 +188,17 @@ __device__ __forceinline__ uint32_t wave_item_end(const AttendArgs& a) {
     return a.csr_hdr ? __builtin_amdgcn_readfirstlane(a.csr_hdr[1]) : a.n_group_items + a.n_wave_items;
 }
 
-// Wave item idx of a CSR call, derived from the tables: idx = (slot * hkv +
-// kv_head) * nrb + row block; slot is chunk k of sequence b, pages
-// indptr[b] + k * chunk .. (the last chunk ends at b's last page).
+// Wave item idx of a CSR call, derived from the tables: idx = (j * hkv +
+// kv_head) * nrb + row block; seqslots[j] names the j-th chunk in dispatch
+// order, chunk k of sequence b in slot slot_ptr[b] + k, pages
+// indptr[b] + k * chunk .. (the last chunk ends at b's last page).  seq_off
+// = j: the row's slot is read back from seqslots[j] (row_target).
 __device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
     const uint32_t nrb = a.csr_nrb, per = a.hkv * nrb;
-    const uint32_t slot = idx / per, rem = idx - slot * per;
+    const uint32_t j = idx / per, rem = idx - j * per;
     const uint32_t h = rem / nrb, rb = rem - h * nrb;
-    const uint32_t b = __builtin_amdgcn_readfirstlane(a.seqslots[slot].seq);
+    const uint32_t b = __builtin_amdgcn_readfirstlane(a.seqslots[j].seq);
+    const uint32_t slot = __builtin_amdgcn_readfirstlane(a.seqslots[j].slot);
     const uint32_t chunk = __builtin_amdgcn_readfirstlane(a.csr_hdr[0]);
     const uint32_t k = slot - __builtin_amdgcn_readfirstlane(a.csr_slot_ptr[b]);
     const uint32_t p0 = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b]));
@@ -203,7 +206,7 @@ __device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
     Item it;
     it.page_off = p0 + k * chunk;
     it.npages = min(chunk, n - k * chunk);
-    it.seq_off = slot;
+    it.seq_off = j;
     it.row_begin = rb * kWaveRows;
     it.nrows = min(uint32_t(kWaveRows), a.r - rb * kWaveRows);
     it.kv_head = h;
@@ -2377,6 +2380,22 @@ __device__ __forceinline__ void merge_row(const void* ws_o, const PartialLse* ws
             return;
         }
     }
+    if constexpr (NV < 0) {   // loads per pass from the row's own state count (wave-uniform)
+        using MS = MergeShape<D, OUT>;
+        constexpr int S = MS::SPI, MX = MS::MAX_NV;
+        if (n <= uint32_t(S)) {
+            merge_row_v<D, OUT, 1>(ws_o, ws_lse, out, hq, b, qh, s0, n, lane);
+            return;
+        }
+        if (n <= uint32_t(4 * S)) {
+            merge_row_v<D, OUT, (MX < 4 ? MX : 4)>(ws_o, ws_lse, out, hq, b, qh, s0, n, lane);
+            return;
+        }
+        if (n <= 64) {
+            merge_row_v<D, OUT, MX>(ws_o, ws_lse, out, hq, b, qh, s0, n, lane);
+            return;
+        }
+    }
     constexpr int U = NV == 0 ? 32 : 16;
     constexpr int PL = D / 64;
     float acc[PL];
@@ -2476,93 +2495,322 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------- decode from device CSR
-// Inclusive prefix sum of v over a workgroup of kCsrThreads threads; total
-// receives the workgroup's sum.  wsum: LDS, one word per wave.
-constexpr int kCsrThreads = 1024;
+// The CSR planning kernel runs as one workgroup of NT threads: one wave for
+// batches of at most 64 sequences (one sequence a lane, no barriers between
+// its passes), one wave per SIMD (256 threads) beyond.  Each thread keeps
+// the page counts of its first csr_reg_seqs(NT) sequences in registers
+// across the passes (the small variant's code stays short: it runs on a CU
+// whose instruction cache has not seen it).
+constexpr uint32_t kCsrSmallThreads = 64, kCsrThreads = 256;
+constexpr uint32_t csr_reg_seqs(uint32_t nt) { return nt == kCsrSmallThreads ? 1u : 2u; }
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(v, o, 64);
-        if (lane >= o) v += t;
-    }
-    return v;
+// Inclusive scan over the wave (lane i: the sum, or minimum, of lanes
+// 0..i): row shifts by 1, 2, 4, 8 within each 16-lane row, then the last
+// lane of row 0 / 2 into rows 1 / 3 (row_bcast:15) and of row 1 into rows
+// 2 and 3 (row_bcast:31).  A lane whose source is outside its row, or whose
+// row is masked off, takes the identity.  Every lane must be active.
+template <bool MIN>
+__device__ __forceinline__ uint32_t wave_scan_dpp(uint32_t x) {
+    const int id = MIN ? -1 : 0;
+    auto op = [](uint32_t u, int v) { return MIN ? min(u, uint32_t(v)) : u + uint32_t(v); };
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x111, 0xf, 0xf, false));   // row_shr:1
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x112, 0xf, 0xf, false));   // row_shr:2
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x114, 0xf, 0xf, false));   // row_shr:4
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x118, 0xf, 0xf, false));   // row_shr:8
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x142, 0xa, 0xf, false));   // row_bcast:15
+    x = op(x, __builtin_amdgcn_update_dpp(id, int(x), 0x143, 0xc, 0xf, false));   // row_bcast:31
+    return x;
 }
 
-__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+// Inclusive prefix sums of x and y over the workgroup; tx / ty receive the
+// totals.  lds: 2 * NT / 64 words.
+template <uint32_t NT>
+__device__ __forceinline__ void block_incl_scan2(uint32_t& x, uint32_t& y, uint32_t* lds, uint32_t& tx,
+                                                 uint32_t& ty) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int NW = kCsrThreads / 64;
-    v = wave_incl_scan(v, lane);
-    if (lane == 63) wsum[wave] = v;
-    __syncthreads();
-    if (wave == 0) {
-        uint32_t x = lane < NW ? wsum[lane] : 0u;
-        x = wave_incl_scan(x, lane);
-        if (lane < NW) wsum[lane] = x;
+    x = wave_scan_dpp<false>(x);
+    y = wave_scan_dpp<false>(y);
+    if constexpr (NT == 64) {
+        tx = __builtin_amdgcn_readlane(x, 63);
+        ty = __builtin_amdgcn_readlane(y, 63);
+    } else {
+        constexpr int NW = NT / 64;
+        if (lane == 63) {
+            lds[wave] = x;
+            lds[NW + wave] = y;
+        }
+        __syncthreads();
+        uint32_t bx = 0, by = 0;
+        #pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const uint32_t a = lds[w], b = lds[NW + w];
+            bx += w < wave ? a : 0u;
+            by += w < wave ? b : 0u;
+            tx = w == 0 ? a : tx + a;
+            ty = w == 0 ? b : ty + b;
+        }
+        x += bx;
+        y += by;
+        __syncthreads();
     }
-    __syncthreads();
-    const uint32_t r = v + (wave ? wsum[wave - 1] : 0u);
-    total = wsum[NW - 1];
-    __syncthreads();
-    return r;
 }
+
+// Workgroup reduction of K values per thread (MIN: minima, else sums);
+// every thread receives the results.  lds: NT / 64 * K words.
+// Only the values whose bit is set in `active` (uniform) are reduced.
+template <uint32_t NT, bool MIN, uint32_t K>
+__device__ __forceinline__ void block_reduce(uint32_t (&v)[K], uint32_t* lds, uint64_t active = ~uint64_t(0)) {
+    #pragma unroll
+    for (uint32_t i = 0; i < K; ++i)
+        if ((active >> i) & 1u) v[i] = __builtin_amdgcn_readlane(wave_scan_dpp<MIN>(v[i]), 63);
+    if constexpr (NT > 64) {
+        constexpr uint32_t NW = NT / 64;
+        const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+        if (lane == 0) {
+            #pragma unroll
+            for (uint32_t i = 0; i < K; ++i)
+                if ((active >> i) & 1u) lds[wave * K + i] = v[i];
+        }
+        __syncthreads();
+        #pragma unroll
+        for (uint32_t i = 0; i < K; ++i) {
+            if (!((active >> i) & 1u)) continue;
+            uint32_t s = lds[i];
+            #pragma unroll
+            for (uint32_t w = 1; w < NW; ++w) s = MIN ? min(s, lds[w * K + i]) : s + lds[w * K + i];
+            v[i] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// Chunk sizes (pages) a CSR call weighs: thirteen fixed ones and the size
+// that gives one wave per wave slot.  An item costs kCsrStartPairs plus its
+// page pairs (the planner's cost model for wave items).
+constexpr uint32_t kCsrFixedCandidates = 13, kCsrStartPairs = 3, kCsrMaxStates = 64;
+
+__device__ __forceinline__ uint32_t csr_candidate(uint32_t i) {
+    switch (i) {
+    case 0: return 1u;
+    case 1: return 2u;
+    case 2: return 4u;
+    case 3: return 8u;
+    case 4: return 16u;
+    case 5: return 32u;
+    case 6: return 48u;
+    case 7: return 64u;
+    case 8: return 96u;
+    case 9: return 128u;
+    case 10: return 160u;
+    case 11: return 192u;
+    default: return 256u;
+    }
+}
+
+__device__ __forceinline__ uint32_t csr_cost(uint32_t pages) { return kCsrStartPairs + (pages + 1) / 2; }
 
 // Work decomposition of one dh_decode_csr call, on the device: sequence b's
-// pages indptr[b] .. indptr[b+1] split into chunks of `chunk` pages, chunk k
-// of b in partial-state slot slot_ptr[b] + k.  chunk is the largest of 8,
-// the size that gives about kCsrTargetWaves wave items, and the size that
-// keeps the slots within the workspace; past kCsrMaxChunk pages the tables do
-// not fit (overflow: no items, zeros out).  A sequence whose indptr entries
-// are negative or decreasing, or that has more than DH_MAX_SEQ_LEN / 16
-// pages, gets no chunk and is marked bad (zeros out, status DH_EINVAL).
-__global__ __launch_bounds__(kCsrThreads) void csr_plan_kernel(CsrPlanArgs p) {
-    __shared__ uint32_t wsum[kCsrThreads / 64];
+// pages indptr[b] .. indptr[b+1] split into chunks of `chunk` pages (the last
+// one shorter), chunk k of b in partial-state slot slot_ptr[b] + k.
+//
+// chunk: of the candidates whose chunks fit the workspace's slots, the one
+// whose heaviest-first list schedule over kCsrWaveSlots wave slots is
+// estimated to end first (ties: the larger chunk, fewer partial states).  The
+// estimate is the largest item when the waves fit the slots at once, else
+// the mean load plus the smallest item (the last ones placed), at least the
+// largest item.  On 35 batches of 1-600 sequences it picks a chunk whose
+// exact heaviest-first schedule ends 3 % after the best candidate's on
+// average.  Chunks that give a sequence more than kCsrMaxStates partial
+// states come last (C2, six 272-page sequences: 4-page chunks, 68 states a
+// row, took the merge from the vector to the scalar path).  No candidate
+// fitting (more chunks of kCsrMaxChunk pages than the workspace holds):
+// overflow, no items, zeros out.
+//
+// Dispatch order (seqslots[j] = {sequence, slot} of the j-th chunk, j the
+// wave item's index / per_chunk): the full chunks first, then the shorter
+// last chunks by size, longest first, so the hardware's in-order dispatch
+// to free slots is a heaviest-first list schedule.  Order does not change
+// results: each chunk's partial state has its slot, merged in slot order.
+//
+// A sequence whose indptr entries are negative or decreasing, or that has
+// more than DH_MAX_SEQ_LEN / 16 pages, gets no chunk and is marked bad
+// (zeros out, status DH_EINVAL).
+template <uint32_t NT>
+__global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
+    constexpr uint32_t KC = kCsrFixedCandidates, KM = KC + 1;
+    __shared__ uint32_t red[(NT / 64) * 2 * KM];
+    __shared__ uint32_t s_tail[kCsrMaxChunk];    // last chunks of each size, then their next position
     const uint32_t tid = threadIdx.x;
     constexpr uint32_t kMaxSeqPages = DH_MAX_SEQ_LEN / kPageSize;
-    auto seq_pages = [&](uint32_t b, bool& ok) -> uint32_t {
+    const uint32_t iters = (p.batch + NT - 1) / NT;
+    auto load = [&](uint32_t b, bool& ok) -> uint32_t {
+        ok = false;
+        if (b >= p.batch) return 0u;
         const int32_t p0 = p.indptr[b], p1 = p.indptr[b + 1];
         ok = p0 >= 0 && p1 >= p0 && uint32_t(p1 - p0) <= kMaxSeqPages;
         return ok ? uint32_t(p1 - p0) : 0u;
     };
-    // Pass 1: pages of the valid sequences (<= 2^16 * 2^13, fits 32 bits).
-    uint32_t total = 0;
-    for (uint32_t base = 0; base < p.batch; base += kCsrThreads) {
+    constexpr uint32_t R = csr_reg_seqs(NT);
+    uint32_t nr[R], okr = 0;
+    #pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
         bool ok = false;
-        const uint32_t n = base + tid < p.batch ? seq_pages(base + tid, ok) : 0u;
-        uint32_t t;
-        block_incl_scan(n, wsum, t);
-        total += t;
+        nr[r] = load(r * NT + tid, ok);
+        okr |= ok ? 1u << r : 0u;
     }
-    const uint64_t want = (uint64_t(total) * p.per_chunk + kCsrTargetWaves - 1) / kCsrTargetWaves;
-    const uint64_t fit = (uint64_t(total) + (p.slot_cap - p.batch) - 1) / (p.slot_cap - p.batch);
-    uint32_t chunk = uint32_t(max(uint64_t(kCsrMinChunk), max(want, fit)));
-    chunk = min(chunk, kCsrMaxChunk);
-    // Pass 2: chunk counts, their prefix sum, the slots' sequences.
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < p.batch; base += kCsrThreads) {
-        const uint32_t b = base + tid;
-        bool ok = false;
-        const uint32_t n = b < p.batch ? seq_pages(b, ok) : 0u;
-        const uint32_t cnt = (n + chunk - 1) / chunk;
-        uint32_t t;
-        const uint32_t first = carry + block_incl_scan(cnt, wsum, t) - cnt;
+    // f(b, n, ok) over this thread's sequences in order, with a trip count
+    // uniform over the workgroup (f may hold barriers); b >= batch: n = 0.
+    auto each = [&](auto&& f) {
+        #pragma unroll
+        for (uint32_t r = 0; r < R; ++r)
+            if (r < iters) f(r * NT + tid, nr[r], ((okr >> r) & 1u) != 0u);
+        if constexpr (NT > kCsrSmallThreads) {
+            for (uint32_t it = R; it < iters; ++it) {
+                bool ok = false;
+                const uint32_t b = it * NT + tid;
+                const uint32_t n = load(b, ok);
+                f(b, n, ok);
+            }
+        }
+    };
+    for (uint32_t i = tid; i < kCsrMaxChunk; i += NT) s_tail[i] = 0u;
+
+    // Pass 1: pages in all (<= 2^16 * 2^13; the costs below, at most 4 a
+    // page, fit 32 bits) and the longest sequence.
+    uint32_t tot[1] = {0u}, nmax[1] = {~0u};
+    each([&](uint32_t, uint32_t n, bool) {
+        tot[0] += n;
+        nmax[0] = min(nmax[0], ~n);
+    });
+    block_reduce<NT, false>(tot, red);
+    block_reduce<NT, true>(nmax, red);
+    const uint32_t total = tot[0], maxn = ~nmax[0];
+    const uint32_t want = uint32_t(min(uint64_t(kCsrMaxChunk),
+                                       max(uint64_t(1), (uint64_t(total) * p.per_chunk + kCsrWaveSlots - 1) /
+                                                            kCsrWaveSlots)));
+    // Candidates weighed (bit i: fixed candidate i; bit KC: want): the fixed
+    // sizes from want / 8 up to want (a larger chunk costs more per item and
+    // balances no better than want's; below want / 8 an item start costs
+    // more than its pages), the smallest fixed size that leaves a sequence
+    // at most kCsrMaxStates states, kCsrMaxChunk (the fallback) and want.
+    const uint32_t need = (maxn + kCsrMaxStates - 1) / kCsrMaxStates;
+    uint32_t active = (1u << (KC - 1)) | (1u << KC);
+    bool need_met = false;
+    #pragma unroll
+    for (uint32_t i = 0; i < KC; ++i) {
+        const uint32_t c = csr_candidate(i);
+        if (8 * c >= want && c <= want) active |= 1u << i;
+        if (!need_met && c >= need) {
+            active |= 1u << i;
+            need_met = true;
+        }
+    }
+    // Pass 2: per candidate, its chunks, their cost and the cheapest chunk.
+    uint32_t sums[2 * KM] = {}, mins[KM];
+    #pragma unroll
+    for (uint32_t i = 0; i < KM; ++i) mins[i] = ~0u;
+    each([&](uint32_t, uint32_t n, bool) {
+        if (n == 0) return;
+        #pragma unroll
+        for (uint32_t i = 0; i < KM; ++i) {
+            if (!((active >> i) & 1u)) continue;
+            const uint32_t c = i < KC ? csr_candidate(i) : want, full = n / c, t = n - full * c;
+            sums[i] += full + (t ? 1u : 0u);
+            sums[KM + i] += full * csr_cost(c) + (t ? csr_cost(t) : 0u);
+            mins[i] = min(mins[i], csr_cost(t ? t : c));
+        }
+    });
+    block_reduce<NT, false>(sums, red, uint64_t(active) | (uint64_t(active) << KM));
+    block_reduce<NT, true>(mins, red, active);
+
+    // Chunks that leave a row more than kCsrMaxStates partial states (the
+    // merge kernel's vector path) rank after every other fitting one.
+    auto end_of = [&](uint32_t c, uint32_t cnt, uint32_t cost, uint32_t mn) -> uint64_t {
+        if (cnt > p.slot_cap) return ~uint64_t(0);
+        const uint64_t S = kCsrWaveSlots, mx = csr_cost(min(c, maxn));
+        const uint64_t e = uint64_t(cnt) * p.per_chunk <= S
+                               ? mx * S
+                               : max(mx * S, uint64_t(cost) * p.per_chunk + uint64_t(mn) * S);
+        return c < need ? e | (uint64_t(1) << 62) : e;     // more than kCsrMaxStates chunks of maxn pages
+    };
+    uint32_t chunk = kCsrMaxChunk, n_chunks = sums[KC - 1];
+    uint64_t best = ~uint64_t(0);
+    #pragma unroll
+    for (uint32_t i = 0; i < KM; ++i) {
+        if (!((active >> i) & 1u)) continue;
+        const uint32_t c = i < KC ? csr_candidate(i) : want;
+        const uint64_t e = end_of(c, sums[i], sums[KM + i], mins[i]);
+        if (e < best || (e == best && e != ~uint64_t(0) && c > chunk)) {
+            best = e;
+            chunk = c;
+            n_chunks = sums[i];
+        }
+    }
+    const bool overflow = n_chunks > p.slot_cap;
+
+    // Pass 3: last chunks of each size; those of size t take the positions
+    // n_chunks - (last chunks of size <= t) onwards, so the longest follow
+    // the full chunks and the shortest end the order.
+    each([&](uint32_t, uint32_t n, bool) {
+        const uint32_t t = n - (n / chunk) * chunk;
+        if (t) atomicAdd(&s_tail[t], 1u);
+    });
+    __syncthreads();
+    {
+        uint32_t carry = 0;
+        for (uint32_t base = 1; base < chunk; base += NT) {
+            const uint32_t t = base + tid;
+            uint32_t v = t < chunk ? s_tail[t] : 0u, z = 0u, tv, tz;
+            block_incl_scan2<NT>(v, z, red, tv, tz);
+            if (t < chunk) s_tail[t] = n_chunks - (carry + v);
+            carry += tv;
+        }
+        __syncthreads();
+    }
+
+    // Pass 4: each sequence's first slot (prefix sum of the chunk counts)
+    // and its chunks' positions: full chunks after the full chunks of the
+    // sequences before it, its last chunk from its size's range.
+    uint32_t carry = 0, carry_t = 0;
+    each([&](uint32_t b, uint32_t n, bool ok) {
+        const uint32_t full = n / chunk, t = n - full * chunk, has_t = t ? 1u : 0u, cnt = full + has_t;
+        uint32_t x = cnt, y = has_t, tx, ty;
+        block_incl_scan2<NT>(x, y, red, tx, ty);
+        const uint32_t first = carry + x - cnt;
+        const uint32_t fpos = first - (carry_t + y - has_t);
         if (b < p.batch) {
             p.slot_ptr[b] = first;
-            p.seq_bad[b] = ok ? 0u : 1u;
-            for (uint32_t k = 0; k < cnt && first + k < p.slot_cap; ++k)
-                p.seqslots[first + k] = SeqSlot{b, first + k};
+            p.seq_bad[b] = (ok && !overflow) ? 0u : 1u;
+            if (!overflow && t) {
+                const uint32_t pos = atomicAdd(&s_tail[t], 1u);
+                if (pos < p.slot_cap) p.seqslots[pos] = SeqSlot{b, first + full};
+            }
         }
-        carry += t;
-    }
-    const bool overflow = carry > p.slot_cap;
-    if (overflow)
-        for (uint32_t b = tid; b < p.batch; b += kCsrThreads) p.seq_bad[b] = 1u;
+        // Full chunks: each lane its own sequence's, or, in the one-wave
+        // variant when a sequence has more of them than there are
+        // sequences, the whole wave one sequence's after another.
+        bool by_wave = false;
+        if constexpr (NT == kCsrSmallThreads)
+            by_wave = ~uint32_t(__builtin_amdgcn_readlane(wave_scan_dpp<true>(~full), 63)) > p.batch;
+        if (!overflow && by_wave) {
+            for (uint32_t sq = 0; sq < p.batch; ++sq) {
+                const uint32_t fs = __builtin_amdgcn_readlane(full, sq), ps = __builtin_amdgcn_readlane(fpos, sq);
+                const uint32_t ss = __builtin_amdgcn_readlane(first, sq);
+                for (uint32_t k = tid; k < fs && ps + k < p.slot_cap; k += kCsrSmallThreads)
+                    p.seqslots[ps + k] = SeqSlot{sq, ss + k};
+            }
+        } else if (!overflow && b < p.batch) {
+            for (uint32_t k = 0; k < full && fpos + k < p.slot_cap; ++k) p.seqslots[fpos + k] = SeqSlot{b, first + k};
+        }
+        carry += tx;
+        carry_t += ty;
+    });
     if (tid == 0) {
-        p.slot_ptr[p.batch] = overflow ? 0u : carry;
+        p.slot_ptr[p.batch] = overflow ? 0u : n_chunks;
         p.hdr->chunk = chunk;
-        p.hdr->n_items = overflow ? 0u : carry * p.per_chunk;
+        p.hdr->n_items = overflow ? 0u : n_chunks * p.per_chunk;
         p.hdr->overflow = overflow ? 1u : 0u;
-        p.hdr->n_chunks = carry;
+        p.hdr->n_chunks = n_chunks;
     }
 }
 
@@ -2679,14 +2927,16 @@ hipError_t launch_merge_d(const MergeArgs& a, uint32_t q_dtype, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     dim3 grid((rows + 3) / 4), block(256);
     // Rows of 17-32 states: the scalar form, one pass of 32.  Otherwise the
-    // vector form with loads per pass for the plan's most states per row (0:
-    // not known on the host, up to 64), so a row loads no state twice.
-    const int states = a.max_states == 0 || a.max_states > 64 ? 64 : int(a.max_states);
+    // vector form with loads per pass for the plan's most states per row, so
+    // a row loads no state twice; not known on the host (0, the CSR path):
+    // chosen per row from its own count.
+    const int states = a.max_states > 64 ? 64 : int(a.max_states);
     auto go = [&](auto out_tag) {
         constexpr uint32_t OUT = decltype(out_tag)::value;
         using MS = MergeShape<D, OUT>;
         const int need = (states + MS::SPI - 1) / MS::SPI;
-        if (states > 16 && states <= 32) hipLaunchKernelGGL((merge_kernel<D, OUT, 0>), grid, block, 0, s, a);
+        if (states == 0) hipLaunchKernelGGL((merge_kernel<D, OUT, -1>), grid, block, 0, s, a);
+        else if (states > 16 && states <= 32) hipLaunchKernelGGL((merge_kernel<D, OUT, 0>), grid, block, 0, s, a);
         else if (need <= 1) hipLaunchKernelGGL((merge_kernel<D, OUT, 1>), grid, block, 0, s, a);
         else if (need <= 2 && MS::MAX_NV >= 2) hipLaunchKernelGGL((merge_kernel<D, OUT, (MS::MAX_NV >= 2 ? 2 : 1)>), grid, block, 0, s, a);
         else if (need <= 4 && MS::MAX_NV >= 4) hipLaunchKernelGGL((merge_kernel<D, OUT, (MS::MAX_NV >= 4 ? 4 : 1)>), grid, block, 0, s, a);
@@ -2739,7 +2989,11 @@ int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint3
 
 int launch_csr_plan(const CsrPlanArgs& p, void* stream) {
     if (p.batch == 0 || p.slot_cap <= p.batch) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(csr_plan_kernel, dim3(1), dim3(kCsrThreads), 0, reinterpret_cast<hipStream_t>(stream), p);
+    const auto s = reinterpret_cast<hipStream_t>(stream);
+    if (p.batch <= kCsrSmallThreads)
+        hipLaunchKernelGGL(csr_plan_kernel<kCsrSmallThreads>, dim3(1), dim3(kCsrSmallThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL(csr_plan_kernel<kCsrThreads>, dim3(1), dim3(kCsrThreads), 0, s, p);
     return hipGetLastError();
 }
 

@@ -205,8 +205,10 @@ int launch_gather(const uint8_t* kv, const uint32_t* pages, uint32_t n_pages, ui
                   void* stream);
 bool attend_supported(uint32_t q_dtype, uint32_t kv_format, uint32_t head_dim);
 int launch_csr_plan(const CsrPlanArgs& p, void* stream);
-// Wave-item chunks the CSR path aims for (the planner's item target).
-constexpr uint32_t kCsrTargetWaves = 2048;
-constexpr uint32_t kCsrMinChunk = 8, kCsrMaxChunk = uint32_t(kWaveIdRegs) * 64;   // the wave item's page-id registers
+// Wave slots of the chip the CSR path schedules against (256 CUs x two
+// workgroups x four waves), and its chunk sizes: 1 page up to what a wave
+// item's page-id registers hold.
+constexpr uint32_t kCsrWaveSlots = 2048;
+constexpr uint32_t kCsrMinChunk = 1, kCsrMaxChunk = uint32_t(kWaveIdRegs) * 64;
 }  // namespace dh
 }
