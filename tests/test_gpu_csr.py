@@ -100,6 +100,36 @@ def test_configs(backend, name):
     _check(run, got, run.reference(), name)
 
 
+@pytest.mark.parametrize("case", ["many_short", "one_long", "mixed_64", "wide_lengths"])
+def test_chunk_choice_shapes(backend, case):
+    """Batches that reach the planning kernel's other branches: 1 500
+    sequences (256 threads, page counts re-read past the ones kept in
+    registers, several scan rounds), one 3 000-page sequence (the 64-states
+    rule sets the chunk), 64 sequences with empty ones among them (one wave,
+    full chunks written by the whole wave), 300 sequences of 1-700 pages
+    (every last-chunk size).  Tables draw page ids with repeats, so pages
+    are shared across sequences."""
+    rng = np.random.default_rng({"many_short": 1, "one_long": 2, "mixed_64": 3, "wide_lengths": 4}[case])
+    if case == "many_short":
+        lens = rng.integers(1, 7, 1500)
+    elif case == "one_long":
+        lens = np.array([3000])
+    elif case == "mixed_64":
+        lens = rng.integers(0, 40, 64)
+        lens[::7] = 0
+    else:
+        lens = rng.integers(1, 700, 300)
+    pool_pages = int(max(64, lens.sum() // 2 + 8))
+    tables = [rng.integers(0, pool_pages, int(n)).tolist() for n in lens]
+    lpl = rng.integers(1, 17, len(lens)).astype(np.int32)
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, pool_pages, last_page_len=lpl)
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    assert np.all(got[lens == 0] == 0)
+    _check(run, got, run.reference(), case)
+
+
 def test_c3_full_flat(backend):
     """The headline tree read flat from device tables: every leaf's 536
     pages, all 64 leaves against the oracle."""
