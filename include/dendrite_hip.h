@@ -392,8 +392,9 @@ dh_status dh_decode_batch_static(dh_backend* backend, const dh_pool* pool, const
 /* Workspace bytes dh_decode_csr needs for batch_size sequences whose page
  * tables hold at most max_total_pages entries together (indptr[batch] -
  * indptr[0] <= max_total_pages).  The size grows with batch_size and with
- * max_total_pages up to a cap (about 2048 work items' partial states), so a
- * workspace sized for a long context serves every shorter one.  Replaces
+ * max_total_pages up to a cap (about two waves per wave slot of the chip,
+ * 4 096 work items, in partial states), so a workspace sized for a long
+ * context serves every shorter one.  Replaces
  * BatchDecodeKernel::workspace_size (flashinfer/batch_decode.rs:56-73). */
 size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch_size, uint32_t max_total_pages);
 
@@ -412,10 +413,11 @@ size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch_size, uin
  *                   sequences' outputs are zeros and no page outside the
  *                   pool is read) or DH_ENOMEM (the tables need more work
  *                   items than the workspace holds: every output is zeros).
- * Every sequence is split into chunks of equal page count (chosen on the
- * device from the tables' total, 8 to 256 pages) attended by one wave each
- * and merged by log-sum-exp: a flat batch, without the shared-prefix
- * reuse of a cascade plan.  Host checks (returned synchronously): cfg and
+ * Every sequence is split into chunks of one page count (the last chunk
+ * shorter), chosen on the device from the tables for the earliest estimated
+ * end over the chip's wave slots, 1 to 256 pages.  Each chunk is attended
+ * by one wave and the chunks are merged by log-sum-exp: a flat batch,
+ * without the shared-prefix reuse of a cascade plan.  Host checks (returned synchronously): cfg and
  * pool agree, the pointers are device memory, the workspace holds at least
  * batch + 1 chunks.  Three kernels on `stream`; allocates nothing. */
 dh_status dh_decode_csr(dh_backend* backend, const dh_pool* pool, const dh_attn_config* cfg,
