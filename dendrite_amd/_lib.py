@@ -36,6 +36,7 @@ DIRECT_AUTO, DIRECT_OFF = 0, 1
 
 PAGE_SIZE = 16
 STATIC_WORKSPACE_BYTES = 32 << 20   # DH_STATIC_WORKSPACE_BYTES
+HOST_LENS_MAX_BATCH = 512           # DH_HOST_LENS_MAX_BATCH
 MAX_SEQ_LEN = 131072
 INVALID_PAGE = 0xFFFFFFFF
 INVALID_NODE = 0xFFFFFFFFFFFFFFFF
@@ -125,6 +126,7 @@ SIGNATURES = {
     "dh_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "dh_decode_stages": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _U32, _P]),
     "dh_decode_batch_static": (_I, [_P, _P, _P, _P, _P, _P, _P]),
+    "dh_decode_batch_host_lens": (_I, [_P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "dh_csr_workspace_size": (C.c_size_t, [C.POINTER(dh_attn_config), _U32, _U32]),
     "dh_decode_csr": (_I, [_P, _P, C.POINTER(dh_attn_config), _U32, _P, _P, _P, _P, _P, _P, C.c_size_t, _P,
                            _P]),

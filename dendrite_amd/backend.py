@@ -388,6 +388,20 @@ def decode_batch(plan: DecodePlan, q, out, workspace, last_page_len=None, stream
                                  C.c_void_p(_stream_ptr(stream))))
 
 
+def decode_batch_host_lens(plan: DecodePlan, q, out, workspace, last_page_len=None, stream=None) -> None:
+    """dh_decode_batch_host_lens: dh_decode_batch with the last-page lengths
+    a host int32 array (numpy, or None: all pages full), carried to the
+    kernels in their arguments; at most HOST_LENS_MAX_BATCH sequences."""
+    lpl = None
+    if last_page_len is not None:
+        last_page_len = np.ascontiguousarray(last_page_len, dtype=np.int32)
+        lpl = C.c_void_p(last_page_len.ctypes.data)
+    check(lib().dh_decode_batch_host_lens(plan.backend._h, plan.pool._h, plan._h, C.c_void_p(q.data_ptr()), lpl,
+                                          C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()),
+                                          workspace.numel() * workspace.element_size(),
+                                          C.c_void_p(_stream_ptr(stream))))
+
+
 def csr_workspace_size(config: AttentionConfig, batch_size: int, max_total_pages: int) -> int:
     """dh_csr_workspace_size: workspace bytes of decode_csr."""
     return int(lib().dh_csr_workspace_size(C.byref(config.to_c()), batch_size, max_total_pages))
@@ -884,9 +898,11 @@ class HipBackend:
         q = c.query_batch(queries, (B, H, D), dev)
         lens = self.page_len.array[c.last_ids]
         lens[c.last_empty] = _lib.PAGE_SIZE
-        lpl = c.last_page_lens(lens)
         out = torch.empty((B, H, D), dtype=qdt, device=dev)
-        decode_batch(c.plan, q, out, c.ws, lpl)
+        if B <= _lib.HOST_LENS_MAX_BATCH:    # lengths in the kernel arguments: no upload, no event
+            decode_batch_host_lens(c.plan, q, out, c.ws, lens)
+        else:
+            decode_batch(c.plan, q, out, c.ws, c.last_page_lens(lens))
         return out.view(B, 1, H, 1, D)
 
     def decode(self, query, block_table: BlockTable, config: AttentionConfig):

@@ -862,9 +862,11 @@ static dh_status check_device_ptr(const void* p, const char* what) {
 
 // ws_static: ws is the backend's static scratch (device memory by
 // construction; the runtime does not track module globals as allocations).
+// host_lens: last-page lengths in host memory (dh_decode_batch_host_lens),
+// packed into the kernel arguments; last_page_len is then null.
 static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
                              const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes, uint32_t mask,
-                             void* stream, bool ws_static) {
+                             void* stream, bool ws_static, const int32_t* host_lens = nullptr) {
     if (!be || !pool || !pl) return fail(DH_EINVAL, "NULL argument");
     if (pl->be != be || pool->be != be) return fail(DH_EINVAL, "plan/pool belong to another backend");
     if (pool->num_pages != pl->pool_pages || pool->hkv != pl->cfg.num_kv_heads ||
@@ -901,6 +903,17 @@ static dh_status decode_impl(dh_backend* be, const dh_pool* pool, const dh_plan*
         a.kv = pool->data;
         a.scales = pool->scales;
         a.last_page_len = last_page_len;
+        if (host_lens) {
+            // 4 bits a sequence; 16 and every value outside 1..15 pack as
+            // 0, which the kernels read as a full page (as they read the
+            // device array's out-of-range values).
+            a.lpl_inline = 1u;
+            for (uint32_t b = 0; b < pl->batch; ++b) {
+                const int32_t v = host_lens[b];
+                const uint32_t nib = v >= 1 && v < int32_t(DH_PAGE_SIZE) ? uint32_t(v) : 0u;
+                a.lpl_nib[b >> 3] |= nib << (4 * (b & 7));
+            }
+        }
         a.ws_o = ws_o;
         a.ws_lse = ws_lse;
         a.hq = c.num_heads;
@@ -953,6 +966,16 @@ dh_status dh_decode_batch(dh_backend* be, const dh_pool* pool, const dh_plan* pl
                           const int32_t* last_page_len, void* out, void* ws, size_t ws_bytes,
                           void* stream) {
     return decode_impl(be, pool, pl, q, last_page_len, out, ws, ws_bytes, 3u, stream, false);
+}
+
+dh_status dh_decode_batch_host_lens(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,
+                                    const int32_t* last_page_len_host, void* out, void* ws, size_t ws_bytes,
+                                    void* stream) {
+    if (!pl) return fail(DH_EINVAL, "NULL argument");
+    if (pl->batch > DH_HOST_LENS_MAX_BATCH)
+        return fail(DH_EUNSUPPORTED, "%u sequences: host last-page lengths take at most %u (use dh_decode_batch)",
+                    pl->batch, DH_HOST_LENS_MAX_BATCH);
+    return decode_impl(be, pool, pl, q, nullptr, out, ws, ws_bytes, 3u, stream, false, last_page_len_host);
 }
 
 dh_status dh_decode_batch_static(dh_backend* be, const dh_pool* pool, const dh_plan* pl, const void* q,

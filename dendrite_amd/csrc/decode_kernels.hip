@@ -226,8 +226,14 @@ __device__ __forceinline__ int page_tokens(const Item& it, uint32_t i, int last_
 // fill (full pair / partial pair) a scalar branch instead of a masked
 // execution of both sides.
 __device__ __forceinline__ int item_last_len(const AttendArgs& a, const Item& it) {
-    if (!(it.flags & kItemTail) || a.last_page_len == nullptr) return kPageSize;
-    int L = __builtin_amdgcn_readfirstlane(a.last_page_len[it.tail_seq]);
+    if (!(it.flags & kItemTail)) return kPageSize;
+    int L;
+    if (a.last_page_len)
+        L = __builtin_amdgcn_readfirstlane(a.last_page_len[it.tail_seq]);
+    else if (a.lpl_inline)   // 4 bits a sequence in the kernel arguments, 0 for 16
+        L = int((__builtin_amdgcn_readfirstlane(a.lpl_nib[it.tail_seq >> 3]) >> (4 * (it.tail_seq & 7))) & 15u);
+    else
+        return kPageSize;
     return (L <= 0 || L > kPageSize) ? kPageSize : L;
 }
 

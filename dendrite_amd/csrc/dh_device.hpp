@@ -11,6 +11,7 @@
 #pragma once
 #include <stdint.h>
 #include <stddef.h>
+#include "dendrite_hip.h"
 
 #if defined(__HIPCC__)
 #define DH_HOST_DEVICE __host__ __device__
@@ -132,6 +133,11 @@ struct AttendArgs {
     uint32_t wave_direct;
     const uint32_t* slot_ptr;
     void* out;
+    // Last-page lengths carried in the kernel arguments (a host array at the
+    // call, dh_decode_batch_host_lens): 4 bits per sequence, 0 meaning 16;
+    // read when last_page_len is null and lpl_inline is 1.
+    uint32_t lpl_inline;
+    uint32_t lpl_nib[DH_HOST_LENS_MAX_BATCH / 8];
 };
 
 // What the CSR planning kernel leaves in the workspace for the attention

@@ -369,6 +369,24 @@ dh_status dh_decode_batch(dh_backend* backend, const dh_pool* pool,
                           const int32_t* last_page_len, void* out,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Most sequences dh_decode_batch_host_lens takes. */
+#define DH_HOST_LENS_MAX_BATCH 512u
+
+/* dh_decode_batch with the last-page lengths read from host memory during
+ * the call and carried to the kernels in their arguments (4 bits each): no
+ * upload, no event, and the array may be reused as soon as the call
+ * returns.  For callers whose lengths are host state that changes every
+ * step, like the trait's decode_batch, which derives them from host block
+ * tables (attention/backend.rs:80-85, 267-283).  last_page_len_host:
+ * int32[batch] in host memory, or NULL (all pages full); values as for
+ * dh_decode_batch (1..16; 0 or anything outside 1..16 reads as 16).
+ * Plans of more than DH_HOST_LENS_MAX_BATCH sequences are DH_EUNSUPPORTED
+ * (use dh_decode_batch).  Other arguments and results as dh_decode_batch;
+ * allocates nothing. */
+dh_status dh_decode_batch_host_lens(dh_backend* backend, const dh_pool* pool, const dh_plan* plan,
+                                    const void* q, const int32_t* last_page_len_host, void* out,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of the static scratch array behind dh_decode_batch_static (per GPU). */
 #define DH_STATIC_WORKSPACE_BYTES (32u << 20)
 

@@ -222,3 +222,38 @@ def test_rows_with_many_partial_states(backend):
     tables = [list(range(150)), list(range(70)) + [200, 201], [300], list(range(310, 330))]
     w = workloads.custom(tables, 32, 8, 128, _lib.DTYPE_BF16, _lib.KV_BF16, 400, last_page_len=[7, 16, 2, 11])
     _check(w, backend, shared_chunk_pages=1, private_chunk_pages=1)
+
+
+@pytest.mark.parametrize("name", ["c3small", "c4small", "c2"])
+def test_host_last_page_lengths(backend, name):
+    """dh_decode_batch_host_lens (lengths read from host memory, carried in
+    the kernel arguments) gives the same bits as dh_decode_batch with the
+    same lengths on the device: the workload's own, every value 1-16, and
+    the out-of-range values both read as a full page (0, -3, 17); NULL as
+    all pages full.  More than DH_HOST_LENS_MAX_BATCH sequences are
+    DH_EUNSUPPORTED."""
+    import torch
+    from dendrite_amd.backend import DecodePlan, DhError, decode_batch, decode_batch_host_lens
+    w = {"c3small": lambda: workloads.c3(root_pages=40, levels=2, level_pages=3, pool_pages=4096),
+         "c4small": lambda: workloads.c4(n_seqs=24, tmin=40, tmax=700, pool_pages=4096),
+         "c2": lambda: workloads.c2()}[name]()
+    run = GpuRun(w, backend)
+    rng = np.random.default_rng(5)
+    for lens in (w.last_page_len, rng.integers(1, 17, w.batch), rng.choice([0, -3, 17, 16, 1], w.batch), None):
+        dev = None if lens is None else torch.from_numpy(np.asarray(lens, dtype=np.int32)).to("cuda:0")
+        run.out.fill_(float("nan"))
+        decode_batch(run.plan, run.q, run.out, run.ws, dev)
+        want = run.out.clone()
+        run.out.fill_(float("nan"))
+        decode_batch_host_lens(run.plan, run.q, run.out, run.ws, lens)
+        torch.cuda.synchronize()
+        assert torch.equal(run.out.view(torch.uint8), want.view(torch.uint8))
+    got = run.run()
+    assert excess_err(got, run.reference(), w.q_dtype) <= TOL[w.q_dtype]
+    tables = [[int(p) for p in w.seq_pages(b % w.batch)] for b in range(_lib.HOST_LENS_MAX_BATCH + 1)]
+    big = workloads.custom(tables, w.hq, w.hkv, w.d, w.q_dtype, w.kv_format, w.num_pool_pages)
+    plan = DecodePlan(backend, big.attention_config(), run.pool, big.indptr, big.indices)
+    q = torch.zeros((big.batch, w.hq, w.d), dtype=run.q.dtype, device="cuda:0")
+    with pytest.raises(DhError) as e:
+        decode_batch_host_lens(plan, q, torch.empty_like(q), plan.workspace(), np.full(big.batch, 16, np.int32))
+    assert e.value.status == _lib.DH_EUNSUPPORTED
