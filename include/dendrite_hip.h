@@ -359,8 +359,9 @@ dh_status dh_plan_create_prefill(dh_backend* backend, const dh_attn_config* cfg,
  *                   page, the value PageTable::last_page_len reports for one
  *                   (cache/paged.rs:384-390).  Must be GPU-accessible memory
  *                   (a host array, e.g. from dh_tree_last_page_len, is copied
- *                   to the device first); q, out, the workspace and it are
- *                   checked and a pageable host pointer is DH_EINVAL.
+ *                   to the device first, or passed to
+ *                   dh_decode_batch_host_lens); q, out, the workspace and it
+ *                   are checked and a pageable host pointer is DH_EINVAL.
  *   workspace     : device, >= dh_plan_workspace_size(plan) bytes.
  * Replaces BatchDecodeKernel::run (batch_decode.rs:86-101) and
  * CascadeAttention::run (cascade.rs:84-101).  Allocates nothing. */
