@@ -62,8 +62,14 @@ def _as_torch_stream(stream):
 
 
 def _stream_ptr(stream) -> Optional[int]:
+    """The hipStream_t of `stream` (a torch stream or a raw handle); None:
+    torch's current stream on the current device (read through torch's raw
+    accessor, which builds no Stream object, when this build has it)."""
     if stream is None:
         torch = _torch()
+        raw, dev = getattr(torch._C, "_cuda_getCurrentRawStream", None), getattr(torch._C, "_cuda_getDevice", None)
+        if raw is not None and dev is not None:
+            return raw(dev())
         return torch.cuda.current_stream().cuda_stream
     return stream if isinstance(stream, int) else stream.cuda_stream
 
