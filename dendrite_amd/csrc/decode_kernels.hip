@@ -2699,13 +2699,16 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     // balances no better than want's; below want / 8 an item start costs
     // more than its pages), the smallest fixed size that leaves a sequence
     // at most kCsrMaxStates states, kCsrMaxChunk (the fallback) and want.
+    // Sizes below that smallest one are not weighed: they rank after it
+    // (more states a row) and need more slots, and it is at most
+    // DH_MAX_SEQ_LEN / 16 / kCsrMaxStates = 128 pages, a fixed candidate.
     const uint32_t need = (maxn + kCsrMaxStates - 1) / kCsrMaxStates;
-    uint32_t active = (1u << (KC - 1)) | (1u << KC);
+    uint32_t active = (1u << (KC - 1)) | (want >= need ? 1u << KC : 0u);
     bool need_met = false;
     #pragma unroll
     for (uint32_t i = 0; i < KC; ++i) {
         const uint32_t c = csr_candidate(i);
-        if (8 * c >= want && c <= want) active |= 1u << i;
+        if (8 * c >= want && c <= want && c >= need) active |= 1u << i;
         if (!need_met && c >= need) {
             active |= 1u << i;
             need_met = true;
