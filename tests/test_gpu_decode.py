@@ -257,3 +257,25 @@ def test_host_last_page_lengths(backend, name):
     with pytest.raises(DhError) as e:
         decode_batch_host_lens(plan, q, torch.empty_like(q), plan.workspace(), np.full(big.batch, 16, np.int32))
     assert e.value.status == _lib.DH_EUNSUPPORTED
+
+
+def test_host_last_page_lengths_full_batch(backend):
+    """DH_HOST_LENS_MAX_BATCH sequences, every packed word of the kernel
+    arguments in use: bit-identical to the device lengths, and to the oracle."""
+    import torch
+    from dendrite_amd.backend import decode_batch, decode_batch_host_lens
+    rng = np.random.default_rng(11)
+    n = _lib.HOST_LENS_MAX_BATCH
+    pool_pages = 1024
+    tables = [rng.integers(0, pool_pages, int(k)).tolist() for k in rng.integers(1, 4, n)]
+    lpl = rng.integers(0, 17, n).astype(np.int32)
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, pool_pages, last_page_len=lpl)
+    run = GpuRun(w, backend)
+    decode_batch(run.plan, run.q, run.out, run.ws, run.lpl)
+    want = run.out.clone()
+    run.out.fill_(float("nan"))
+    decode_batch_host_lens(run.plan, run.q, run.out, run.ws, lpl)
+    torch.cuda.synchronize()
+    assert torch.equal(run.out.view(torch.uint8), want.view(torch.uint8))
+    got = run.out.float().cpu().numpy()
+    assert excess_err(got, run.reference(), w.q_dtype) <= TOL[w.q_dtype]
