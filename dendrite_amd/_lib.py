@@ -169,12 +169,20 @@ SIGNATURES = {
     "dh_plan_create_tree": (_I, [_P, C.POINTER(dh_attn_config), _P, _P, _PU64, _U32, _U32,
                                  C.POINTER(dh_plan_options), C.POINTER(_P)]),
     "dh_tree_last_page_len": (_I, [_P, _PU64, _U32, C.POINTER(C.c_int32)]),
+}
+
+# libdendrite_testdata.so (include/dendrite_testdata.h): the tests' and
+# benchmark's seeded input generators, kept out of the backend library.
+TESTDATA_PATH = os.path.join(_PKG, "libdendrite_testdata.so")
+TESTDATA_SIGNATURES = {
+    "dh_testdata_last_error": (C.c_char_p, []),
     "dh_synth_normal": (C.c_double, [_U64, _U64]),
     "dh_synth_fill": (_I, [_P, _U32, _U64, _U64, _U64]),
     "dh_synth_pages": (_I, [_U32, _U32, _U32, _U64, _PU32, _U32, C.c_double, _U32, _P, _P]),
 }
 
 _lib = None
+_testdata = None
 
 
 def lib() -> C.CDLL:
@@ -202,6 +210,26 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def testdata_lib() -> C.CDLL:
+    """Loads the in-tree test-data library (raises if it has not been built)."""
+    global _testdata
+    if _testdata is None:
+        if not os.path.exists(TESTDATA_PATH):
+            raise RuntimeError(f"{TESTDATA_PATH} is missing: build it with `python -m dendrite_amd.build`")
+        L = C.CDLL(TESTDATA_PATH)
+        for name, (res, args) in TESTDATA_SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _testdata = L
+    return _testdata
+
+
+def check_testdata(status: int) -> None:
+    if status != DH_OK:
+        raise DhError(status, testdata_lib().dh_testdata_last_error().decode())
 
 
 def last_error() -> str:

@@ -14,6 +14,7 @@ in libdendrite_hip.so; there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes as C
+import threading
 from typing import Optional, Sequence
 
 import numpy as np
@@ -692,7 +693,14 @@ class HipBackend:
         # append re-quantises the page from all its tokens (a block scale
         # covers the whole page); dropped once the page holds 16 tokens.
         self._shadow: dict = {}
-        self._plans = _PlanCache()
+        # One plan cache per stream: a stream's calls run in order, so its
+        # cached plan may be patched and its workspace reused by the next
+        # call on it, while calls on another stream get their own plan and
+        # workspace.  The lock serialises the host side of the calls (plan
+        # lookup, patching, launch), as the reference's backends guard
+        # their state for &self access from several threads.
+        self._plans: dict = {}
+        self._lock = threading.RLock()
         self.plans_built = 0
         self.plans_patched = 0
         self.plans_reused = 0
@@ -749,6 +757,10 @@ class HipBackend:
 
     def append_kv(self, key, value, block_table: BlockTable, position: int) -> None:
         """key/value: [1, num_kv_heads, n, head_dim]; n + position % 16 <= 16."""
+        with self._lock:
+            self._append_kv(key, value, block_table, position)
+
+    def _append_kv(self, key, value, block_table: BlockTable, position: int) -> None:
         block = block_table.get(position // _lib.PAGE_SIZE)
         if block is None or not block.is_valid():
             return                                   # backend.rs:296-298: no block, no store
@@ -778,9 +790,10 @@ class HipBackend:
         """ReferenceBackend::store_kv (backend.rs:140-143): the block's entry
         becomes key / value ([1, num_kv_heads, n, head_dim], n <= 16), from
         token 0 (overwrite, as the reference's map insert)."""
-        self._set_len(int(block_id), 0)
-        self._shadow.pop(int(block_id), None)
-        self.append_kv(key, value, BlockTable.from_blocks([int(block_id)]), 0)
+        with self._lock:
+            self._set_len(int(block_id), 0)
+            self._shadow.pop(int(block_id), None)
+            self._append_kv(key, value, BlockTable.from_blocks([int(block_id)]), 0)
 
     def get_kv(self, block_id: int):
         """ReferenceBackend::get_kv (backend.rs:135-138): the stored K and V of
@@ -803,8 +816,9 @@ class HipBackend:
     def clear_cache(self) -> None:
         """ReferenceBackend::clear_cache (backend.rs:130-133): every stored
         block is forgotten (decode then skips them, as blocks with no KV)."""
-        self.page_len.clear()
-        self._shadow.clear()
+        with self._lock:
+            self.page_len.clear()
+            self._shadow.clear()
 
     def _kept(self, t: BlockTable) -> np.ndarray:
         """The table's pages decode reads: valid blocks holding tokens, in
@@ -829,13 +843,13 @@ class HipBackend:
         lpl = np.array([self.page_len[int(k[-1])] if len(k) else _lib.PAGE_SIZE for k in kept], dtype=np.int32)
         return indptr, indices, lpl
 
-    def _plan_for(self, tables: Sequence[BlockTable], cfg: AttentionConfig, cfg_key):
-        """The decode plan of these tables: the cached one when neither the
-        tables (uid, version) nor the set of stored blocks changed; patched
-        in place (dh_plan_update) when each page list only gained pages at
-        its end or had its last page replaced; else a new plan."""
+    def _plan_for(self, c: "_PlanCache", tables: Sequence[BlockTable], cfg: AttentionConfig, cfg_key):
+        """The decode plan of these tables in the stream's cache c: the
+        cached one when neither the tables (uid, version) nor the set of
+        stored blocks changed; patched in place (dh_plan_update) when each
+        page list only gained pages at its end or had its last page
+        replaced; else a new plan."""
         from .cache import block_table_mutations
-        c = self._plans
         mut = block_table_mutations()
         if (c.plan is not None and c.mut == mut and c.key[0] == cfg_key and c.key[3] == self.page_len.epoch
                 and len(c.tables) == len(tables) and all(a is b for a, b in zip(c.tables, tables))):
@@ -890,25 +904,30 @@ class HipBackend:
         dev = f"cuda:{self.backend.device}"
         qdt = queries[0].dtype
         cfg_key = (config.num_heads, config.num_kv_heads, config.head_dim, config.scale, config.gqa_mapping, qdt)
-        cfg = self._plans.cfg if self._plans.key is not None and self._plans.key[0] == cfg_key else None
-        if cfg is None:
-            cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
-            cfg.scale = config.scale
-            cfg.sliding_window = config.sliding_window
-            cfg.gqa_mapping = config.gqa_mapping
-            cfg.q_dtype = dtype_code(qdt)
-            cfg.kv_format = self.pool.kv_format
-        c = self._plan_for(block_tables, cfg, cfg_key)
-        c.cfg = cfg
-        B, H, D = len(queries), config.num_heads, config.head_dim
-        q = c.query_batch(queries, (B, H, D), dev)
-        lens = self.page_len.array[c.last_ids]
-        lens[c.last_empty] = _lib.PAGE_SIZE
-        out = torch.empty((B, H, D), dtype=qdt, device=dev)
-        if B <= _lib.HOST_LENS_MAX_BATCH:    # lengths in the kernel arguments: no upload, no event
-            decode_batch_host_lens(c.plan, q, out, c.ws, lens)
-        else:
-            decode_batch(c.plan, q, out, c.ws, c.last_page_lens(lens))
+        stream = _stream_ptr(None)
+        with self._lock:
+            c = self._plans.get(stream)
+            if c is None:
+                c = self._plans[stream] = _PlanCache()
+            cfg = c.cfg if c.key is not None and c.key[0] == cfg_key else None
+            if cfg is None:
+                cfg = AttentionConfig(config.num_heads, config.num_kv_heads, config.head_dim)
+                cfg.scale = config.scale
+                cfg.sliding_window = config.sliding_window
+                cfg.gqa_mapping = config.gqa_mapping
+                cfg.q_dtype = dtype_code(qdt)
+                cfg.kv_format = self.pool.kv_format
+            c = self._plan_for(c, block_tables, cfg, cfg_key)
+            c.cfg = cfg
+            B, H, D = len(queries), config.num_heads, config.head_dim
+            q = c.query_batch(queries, (B, H, D), dev)
+            lens = self.page_len.array[c.last_ids]
+            lens[c.last_empty] = _lib.PAGE_SIZE
+            out = torch.empty((B, H, D), dtype=qdt, device=dev)
+            if B <= _lib.HOST_LENS_MAX_BATCH:    # lengths in the kernel arguments: no upload, no event
+                decode_batch_host_lens(c.plan, q, out, c.ws, lens, stream=stream)
+            else:
+                decode_batch(c.plan, q, out, c.ws, c.last_page_lens(lens), stream=stream)
         return out.view(B, 1, H, 1, D)
 
     def decode(self, query, block_table: BlockTable, config: AttentionConfig):

@@ -1,4 +1,7 @@
-"""Builds libdendrite_hip.so in-tree with hipcc for gfx950.
+"""Builds libdendrite_hip.so in-tree with hipcc for gfx950, and beside it
+libdendrite_testdata.so, the seeded input generators of the tests and
+benchmarks (host code only, include/dendrite_testdata.h; not part of the
+backend).
 
 Usage: python -m dendrite_amd.build  (or dendrite_amd.build.build()).
 Every call compiles from scratch; objects go to dendrite_amd/_build/.
@@ -23,6 +26,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libdendrite_hip.so")
+TESTDATA_LIB = os.path.join(PKG, "libdendrite_testdata.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
@@ -44,7 +48,8 @@ SAN_BUILD = os.path.join(PKG, "_build_san")
 SAN_LIB = os.path.join(SAN_BUILD, "libdendrite_hip.so")
 
 HIP_SOURCES = ["decode_kernels.hip", "write_kernels.hip"]
-HOST_SOURCES = ["api.cpp", "planner.cpp", "block_model.cpp", "synth.cpp"]
+HOST_SOURCES = ["api.cpp", "planner.cpp", "block_model.cpp"]
+TESTDATA_SOURCES = ["synth.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -71,9 +76,15 @@ def build(verbose: bool = False, sanitize: bool = False) -> str:
     for src in HOST_SOURCES:
         obj = os.path.join(bdir, src + ".o")
         jobs.append(([HIPCC, *COMMON, *host_flags, "-c", os.path.join(CSRC, src), "-o", obj], obj))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-        for fut in [ex.submit(_run, cmd) for cmd, _ in jobs]:
+    td_objs = [os.path.join(bdir, src + ".o") for src in TESTDATA_SOURCES]
+    td_jobs = [[HIPCC, *COMMON, *HOST, "-c", os.path.join(CSRC, src), "-o", obj]
+               for src, obj in zip(TESTDATA_SOURCES, td_objs)] if not sanitize else []
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs) + len(td_jobs))) as ex:
+        for fut in [ex.submit(_run, cmd) for cmd in [c for c, _ in jobs] + td_jobs]:
             fut.result()
+    if td_jobs:
+        _run([HIPCC, "-shared", "-o", TESTDATA_LIB + ".tmp", *td_objs, "-lpthread"])
+        os.replace(TESTDATA_LIB + ".tmp", TESTDATA_LIB)
     tmp = lib + ".tmp"
     link_san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
                 "-shared-libsan"] if sanitize else []

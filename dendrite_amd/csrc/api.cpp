@@ -396,6 +396,10 @@ dh_status dh_pool_write_tokens(dh_pool* p, uint32_t page_id, uint32_t tok_offset
     return DH_OK;
 }
 
+// Staging memory dh_pool_write_pages keeps between calls (larger uploads
+// allocate, use and free their own).
+constexpr uint64_t kKeepStage = 16ull << 20;
+
 dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const void* data,
                               const void* scales, void* stream) {
     if (!p || (n && (!ids || !data))) return fail(DH_EINVAL, "NULL argument");
@@ -443,6 +447,15 @@ dh_status dh_pool_write_pages(dh_pool* p, const uint32_t* ids, uint32_t n, const
         st = fail(DH_EHIP, "page upload failed: %s", hipGetErrorString(e));
         (void)hipStreamSynchronize(s);   // nothing queued may still use the staging memory
         (void)hipGetLastError();
+    }
+    // The staging memory is kept for the next call only up to kKeepStage
+    // bytes: an engine that sizes its pool to fill the device does not lose
+    // the memory of one large upload for the pool's lifetime.  Every copy
+    // that read it has completed (the stream was synchronised above).
+    if (p->stage_bytes > kKeepStage) {
+        (void)hipFree(p->stage);
+        p->stage = nullptr;
+        p->stage_bytes = 0;
     }
     return st;
 }
@@ -720,9 +733,9 @@ dh_status dh_plan_create_prefill(dh_backend* be, const dh_attn_config* cfg, cons
     st = check_pool_matches(cfg, pool);
     if (st != DH_OK) return st;
     const bool fp8 = cfg->kv_format == DH_KV_FP8_E4M3 || cfg->kv_format == DH_KV_MXFP8;
-    if (cfg->q_dtype == DH_DTYPE_F32 || (fp8 && (cfg->head_dim == 64 || cfg->q_dtype != DH_DTYPE_BF16)))
-        return fail(DH_EUNSUPPORTED, "prefill takes bf16 / f16 queries over 16-bit KV, and bf16 queries over "
-                    "FP8 / MXFP8 KV at head_dim 128 or 256");
+    if (cfg->q_dtype == DH_DTYPE_F32 || (fp8 && cfg->head_dim == 64))
+        return fail(DH_EUNSUPPORTED, "prefill takes bf16 / f16 queries over 16-bit KV, and over FP8 / MXFP8 KV "
+                    "at head_dim 128 or 256");
     if (batch && (!indptr || !kv_len || !q_len)) return fail(DH_EINVAL, "NULL argument");
     if (batch && indptr[batch] > indptr[0] && !indices) return fail(DH_EINVAL, "indices is NULL");
     dh::PrefillInput in;
@@ -843,20 +856,40 @@ dh_status dh_plan_get_stats(const dh_plan* pl, dh_plan_stats* st) {
 
 // The decode kernels dereference q, out, the workspace and last_page_len on
 // the device; a pageable host pointer there would fault the GPU, so each is
-// checked once per thread and then remembered (a few recently seen device
-// pointers; the check costs a runtime query only for a new pointer).
+// checked against the runtime's allocation records.  Each thread remembers
+// the address ranges of the last few allocations it accepted, so a pointer
+// inside one of them costs no runtime query.  Such a range is not dropped
+// when its allocation is freed: device allocations come from the runtime's
+// own reserved address range, which host mappings do not reuse, and a freed
+// range that is reallocated is device memory again.
 static dh_status check_device_ptr(const void* p, const char* what) {
-    thread_local const void* seen[8] = {};
+    struct Range {
+        uintptr_t lo = 0, hi = 0;
+    };
+    thread_local Range seen[8];
     thread_local unsigned next = 0;
-    for (const void* s : seen)
-        if (s == p) return DH_OK;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    for (const Range& r : seen)
+        if (a >= r.lo && a < r.hi) return DH_OK;
     hipPointerAttribute_t attr;
-    const hipError_t e = hipPointerGetAttributes(&attr, p);
+    hipError_t e = hipPointerGetAttributes(&attr, p);
     if (e != hipSuccess || attr.type == hipMemoryTypeUnregistered) {
         (void)hipGetLastError();
         return fail(DH_EINVAL, "%s is not GPU-accessible memory (copy a host array to the device first)", what);
     }
-    seen[next++ % 8] = p;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+    Range r;
+    if (e == hipSuccess && base && size) {
+        r.lo = reinterpret_cast<uintptr_t>(base);
+        r.hi = r.lo + size;
+    } else {   // accepted, but only this address is remembered
+        (void)hipGetLastError();
+        r.lo = a;
+        r.hi = a + 1;
+    }
+    seen[next++ % 8] = r;
     return DH_OK;
 }
 

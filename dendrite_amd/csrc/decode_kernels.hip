@@ -2899,6 +2899,8 @@ hipError_t launch_prefill_d(const AttendArgs& a, uint32_t n, uint32_t q_dtype, u
     } else if constexpr (D >= 128) {
         if (q_dtype == 1 && kvf == KVF_FP8) hipLaunchKernelGGL((prefill16_kernel<D, KVF_FP8, false>), grid, block, 0, s, a);
         else if (q_dtype == 1 && kvf == KVF_MX) hipLaunchKernelGGL((prefill16_kernel<D, KVF_MX, false>), grid, block, 0, s, a);
+        else if (q_dtype == 0 && kvf == KVF_FP8) hipLaunchKernelGGL((prefill16_kernel<D, KVF_FP8, true>), grid, block, 0, s, a);
+        else if (q_dtype == 0 && kvf == KVF_MX) hipLaunchKernelGGL((prefill16_kernel<D, KVF_MX, true>), grid, block, 0, s, a);
         else return hipErrorInvalidValue;
     } else {
         return hipErrorInvalidValue;

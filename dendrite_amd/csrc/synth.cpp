@@ -1,5 +1,5 @@
 // Seeded synthetic inputs for tests and benchmarks (no counterpart in the
-// reference).  Normals: SplitMix64 counter hash + Box-Muller in double
+// reference; built into libdendrite_testdata.so, not the backend library).  Normals: SplitMix64 counter hash + Box-Muller in double
 // precision, so a value depends only on (seed, index) and any subset of a
 // pool can be generated independently and in parallel.  FP8 encodings follow
 // the OCP FP8 (E4M3 "FN") and OCP MX v1.0 (E8M0 scale) specifications.
@@ -10,11 +10,40 @@
 #include <thread>
 #include <vector>
 
-#include "dh_internal.hpp"
+#include <stdarg.h>
+#include <stdio.h>
 
-using dh::fail;
+#include "dendrite_testdata.h"
 
 namespace {
+
+thread_local char g_error[256];
+
+dh_status fail(dh_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+dh_status fail(dh_status s, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+uint32_t kv_elem_bytes(uint32_t fmt) {
+    switch (fmt) {
+        case DH_KV_F16:
+        case DH_KV_BF16: return 2;
+        case DH_KV_F32: return 4;
+        case DH_KV_FP8_E4M3:
+        case DH_KV_MXFP8: return 1;
+        default: return 0;
+    }
+}
+
+uint64_t kv_scale_bytes(uint32_t fmt, uint32_t hkv, uint32_t d) {
+    if (fmt == DH_KV_FP8_E4M3) return uint64_t(2) * hkv * 4;
+    if (fmt == DH_KV_MXFP8) return uint64_t(2) * hkv * 16 * (d / 32);
+    return 0;
+}
 
 inline uint64_t mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -93,6 +122,8 @@ void parallel_for(uint64_t n, F&& f) {
 
 extern "C" {
 
+const char* dh_testdata_last_error(void) { return g_error; }
+
 double dh_synth_normal(uint64_t seed, uint64_t index) { return normal_at(seed, index); }
 
 dh_status dh_synth_fill(void* out, uint32_t dtype, uint64_t seed, uint64_t first, uint64_t n) {
@@ -111,7 +142,7 @@ dh_status dh_synth_fill(void* out, uint32_t dtype, uint64_t seed, uint64_t first
 
 dh_status dh_synth_pages(uint32_t fmt, uint32_t hkv, uint32_t d, uint64_t seed, const uint32_t* ids,
                          uint32_t n, double outlier, uint32_t outlier_every, void* data, void* scales) {
-    const uint32_t eb = dh::kv_elem_bytes(fmt);
+    const uint32_t eb = kv_elem_bytes(fmt);
     if (eb == 0) return fail(DH_EINVAL, "bad kv_format %u", fmt);
     if (n && (!ids || !data)) return fail(DH_EINVAL, "NULL argument");
     if ((fmt == DH_KV_FP8_E4M3 || fmt == DH_KV_MXFP8) && n && !scales)
@@ -120,7 +151,7 @@ dh_status dh_synth_pages(uint32_t fmt, uint32_t hkv, uint32_t d, uint64_t seed, 
     const uint64_t block = uint64_t(16) * d;              // elements of one (plane, head) block
     const uint64_t elems = 2ull * hkv * block;            // elements per page
     const uint64_t page_bytes = elems * eb;
-    const uint64_t scale_bytes = dh::kv_scale_bytes(fmt, hkv, d);
+    const uint64_t scale_bytes = kv_scale_bytes(fmt, hkv, d);
     parallel_for(n, [&](uint64_t a, uint64_t b) {
         std::vector<float> x(block);
         for (uint64_t i = a; i < b; ++i) {

@@ -16,8 +16,8 @@
 Tree shapes follow what TreeState::fork/append_token produce
 (crates/dendrite-core/src/tree/state.rs:49-113): a child's table is the
 parent's table (shared pages, refcount + 1) followed by its own pages.
-K/V/q values come from dh_synth_* (SplitMix64 + Box-Muller), so a page's
-content depends only on (seed, page id).
+K/V/q values come from dh_synth_* (SplitMix64 + Box-Muller) in
+libdendrite_testdata.so, so a page's content depends only on (seed, page id).
 """
 from __future__ import annotations
 
@@ -28,7 +28,7 @@ from typing import Optional
 import numpy as np
 
 from . import _lib
-from ._lib import check, lib
+from ._lib import check_testdata, testdata_lib
 
 _KV_EB = {_lib.KV_F16: 2, _lib.KV_BF16: 2, _lib.KV_F32: 4, _lib.KV_FP8_E4M3: 1, _lib.KV_MXFP8: 1}
 _Q_EB = {_lib.DTYPE_F16: 2, _lib.DTYPE_BF16: 2, _lib.DTYPE_F32: 4}
@@ -89,7 +89,7 @@ class Workload:
         ids = self.page_ids() if ids is None else np.ascontiguousarray(ids, dtype=np.uint32)
         data = np.empty((len(ids), self.page_bytes), dtype=np.uint8)
         scales = np.empty((len(ids), self.scale_bytes), dtype=np.uint8) if self.scale_bytes else None
-        check(lib().dh_synth_pages(self.kv_format, self.hkv, self.d, self.seed,
+        check_testdata(testdata_lib().dh_synth_pages(self.kv_format, self.hkv, self.d, self.seed,
                                    ids.ctypes.data_as(_lib._PU32), len(ids), float(self.outlier),
                                    self.outlier_every, data.ctypes.data_as(C.c_void_p),
                                    None if scales is None else scales.ctypes.data_as(C.c_void_p)))
@@ -100,7 +100,7 @@ class Workload:
         n = self.batch * self.hq * self.d
         dt = np.float32 if self.q_dtype == _lib.DTYPE_F32 else np.uint16
         q = np.empty(n, dtype=dt)
-        check(lib().dh_synth_fill(q.ctypes.data_as(C.c_void_p), self.q_dtype, self.seed ^ 0x51,
+        check_testdata(testdata_lib().dh_synth_fill(q.ctypes.data_as(C.c_void_p), self.q_dtype, self.seed ^ 0x51,
                                   0, n))
         return q.reshape(self.batch, self.hq, self.d)
 

@@ -173,9 +173,11 @@ dh_status dh_pool_write_tokens(dh_pool* pool, uint32_t page_id, uint32_t tok_off
                                const void* k_scale, const void* v_scale, void* stream);
 /* Bulk upload of whole pages (data + scale records) from host memory:
  * page_ids[i] receives data[i] and scales[i] in the pool layout above.
- * Returns once the pages are written (the stream is synchronised); the
- * staging memory is the pool's own, kept from call to call and grown as
- * needed (uploads into one pool from several threads take turns). */
+ * Returns once the pages are written (the stream is synchronised).  The
+ * upload goes through device staging memory of at most 256 MiB of pages;
+ * the pool keeps up to 16 MiB of it from call to call and frees any larger
+ * staging at the end of the call (uploads into one pool from several
+ * threads take turns). */
 dh_status dh_pool_write_pages(dh_pool* pool, const uint32_t* page_ids, uint32_t n,
                               const void* data, const void* scales, void* stream);
 /* Quantise-on-write from device memory: page_ids[i] (device uint32[n]) of
@@ -334,8 +336,9 @@ dh_status dh_plan_inspect(const dh_attn_config* cfg, uint32_t num_pool_pages,
  * ReferenceBackend::prefill (attention/backend.rs:163-204: q_len = kv_len,
  * causal) and BatchPrefillKernel::run (flashinfer/batch_prefill.rs:86-101,
  * K/V written to pages first); chunked prefill over a cached context is
- * q_len < kv_len.  bf16 / f16 queries; FP8 / MXFP8 KV at head_dim 128 and
- * 256.  chunk_pages: KV pages per work item (0 = chosen from the work:
+ * q_len < kv_len.  bf16 / f16 queries (BatchPrefillConfig.dtype,
+ * flashinfer/batch_prefill.rs:23), over FP8 / MXFP8 KV at head_dim 128 and
+ * 256 as well (codes dequantised to the query's type in the kernel).  chunk_pages: KV pages per work item (0 = chosen from the work:
  * one item per block of queries when those fill the chip, else about 1024
  * items); at most about 2040 whatever is asked (an item's page-id list
  * holds 2048 entries), so longer contexts always take several items.
@@ -445,9 +448,16 @@ dh_status dh_decode_csr(dh_backend* backend, const dh_pool* pool, const dh_attn_
                         void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 
 /* Stages of dh_decode_batch, for profiling: bit 0 = attention items,
- * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3.  A prefill
- * plan in which every query row is one work item's (one partial state per
- * row) has no merge: its attention stage writes out. */
+ * bit 1 = log-sum-exp merge.  dh_decode_batch == stage mask 3.  Two kinds of
+ * plan have no merge launch, and for them bit 0 alone runs the whole step
+ * (attention and any merging, writing out) while bit 1 does nothing:
+ *  - a direct decode plan (dh_plan_stats.direct = 1; DH_DIRECT_AUTO chooses
+ *    one when nothing is shared and the sequences are short): each
+ *    workgroup merges the states of its own rows before it ends;
+ *  - a prefill plan in which every query row is one work item's (one
+ *    partial state per row).
+ * To profile the attention and the merge of a decode step apart, build its
+ * plan with dh_plan_options.direct = DH_DIRECT_OFF. */
 dh_status dh_decode_stages(dh_backend* backend, const dh_pool* pool,
                            const dh_plan* plan, const void* q,
                            const int32_t* last_page_len, void* out,
@@ -468,9 +478,15 @@ dh_status dh_merge_states(const float* o_a, const float* lse_a, const float* o_b
                           const float* lse_b, float* o_out, float* lse_out,
                           uint32_t n_rows, uint32_t head_dim, void* stream);
 
-/* ----------------------------------------------------------- debug gather */
+/* ------------------------------------------------------------- test hooks */
 
-/* Copy the K and V planes of kv head `kv_head` for the pages of a device page
+/* The two entry points of this section have no counterpart in the reference
+ * and replace nothing in its FFI: they expose pieces of the kernels to the
+ * parity tests (page selection, FP8 / MXFP8 dequantisation).  The seeded
+ * input generators of the tests and benchmarks are not part of this library
+ * at all: they live in libdendrite_testdata.so (include/dendrite_testdata.h).
+ *
+ * Copy the K and V planes of kv head `kv_head` for the pages of a device page
  * list into out: [2][n_pages][16][head_dim] elements (K block then V block),
  * skipping DH_INVALID_PAGE entries (the output shrinks accordingly; *n_out
  * receives the pages copied).  Uses the decode kernels' page addressing, so a
@@ -590,32 +606,6 @@ dh_status dh_plan_create_tree(dh_backend* backend, const dh_attn_config* cfg, co
  * first (hipMemcpyAsync on the decode's stream).  DH_EUNSUPPORTED for a tree
  * whose blocks are not DH_PAGE_SIZE tokens. */
 dh_status dh_tree_last_page_len(const dh_tree* tree, const uint64_t* nodes, uint32_t n, int32_t* out);
-
-/* ------------------------------------- synthetic inputs (tests, benchmarks) */
-
-/* No counterpart in the reference: seeded generators for the benchmark
- * configurations, so tests and benchmarks build identical inputs.
- * Normals come from SplitMix64 + Box-Muller in double precision:
- *   dh_synth_normal(seed, index) is a pure function of (seed, index). */
-double dh_synth_normal(uint64_t seed, uint64_t index);
-/* out[i] = N(seed, first + i) converted to `dtype` (dh_dtype, round to nearest
- * even), n elements, host memory, multithreaded. */
-dh_status dh_synth_fill(void* out, uint32_t dtype, uint64_t seed, uint64_t first,
-                        uint64_t n);
-/* Fill whole pool pages on the host in the pool layout for format `kv_format`:
- * page i of the output receives page_ids[i]'s content, a pure function of
- * (seed, page id): K/V ~ N(0,1), then
- *   F32/BF16/F16 : rounded to the element type;
- *   FP8_E4M3     : scale = amax/448 per (page, K|V, head) (1 if amax = 0),
- *                  element = E4M3 RNE of x/scale, saturated to +-448;
- *   MXFP8        : every `outlier_every`-th element (0 = none) replaced by
- *                  +-outlier; per 32-group scale 2^(floor(log2 amax) - 8)
- *                  (E8M0, amax = 0 -> 2^-127), E4M3 RNE saturated.
- * data: n * page_bytes, scales: n * scale_bytes (may be NULL if none). */
-dh_status dh_synth_pages(uint32_t kv_format, uint32_t num_kv_heads, uint32_t head_dim,
-                         uint64_t seed, const uint32_t* page_ids, uint32_t n,
-                         double outlier, uint32_t outlier_every,
-                         void* data, void* scales);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,8 @@
 """The C ABI without a GPU: libdendrite_hip.so loads, exports every function
 include/dendrite_hip.h declares, and its host-side entry points behave as
-documented (no device compute is called here)."""
+documented (no device compute is called here); likewise the test-data
+library (libdendrite_testdata.so, include/dendrite_testdata.h), which the
+backend library does not contain."""
 import ctypes as C
 import math
 import os
@@ -15,10 +17,11 @@ from dendrite_amd.backend import AttentionConfig
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dendrite_hip.h")
+TESTDATA_HEADER = os.path.join(ROOT, "include", "dendrite_testdata.h")
 
 
-def _declared():
-    text = open(HEADER).read()
+def _declared(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
     names = set(re.findall(r"\b(dh_[a-z0-9_]+)\s*\(", text))
     typedefs = set(re.findall(r"typedef\s+(?:struct|enum)?\s*\w*\s*\{?[^;]*?\b(dh_[a-z0-9_]+)\s*;", text))
@@ -33,6 +36,20 @@ def test_library_exports_every_declared_function():
     assert not missing, f"declared but not exported: {missing}"
     # and the ctypes signature table covers them all
     assert not [n for n in names if n not in _lib.SIGNATURES]
+
+
+def test_testdata_library_is_separate():
+    """The seeded generators are declared and exported by the test-data
+    library only: the backend's header and library hold none of them."""
+    T = _lib.testdata_lib()
+    names = _declared(TESTDATA_HEADER)
+    assert {"dh_synth_normal", "dh_synth_fill", "dh_synth_pages", "dh_testdata_last_error"} <= set(names)
+    assert not [n for n in names if not hasattr(T, n)]
+    assert not [n for n in names if n not in _lib.TESTDATA_SIGNATURES]
+    assert not [n for n in _declared() if n.startswith("dh_synth")]
+    assert not [n for n in ("dh_synth_normal", "dh_synth_fill", "dh_synth_pages") if hasattr(_lib.lib(), n)]
+    assert T.dh_synth_pages(99, 1, 64, 0, None, 0, C.c_double(0.0), 0, None, None) == _lib.DH_EINVAL
+    assert b"kv_format" in T.dh_testdata_last_error()
 
 
 def test_version_and_errors():
@@ -70,7 +87,7 @@ def test_no_device_is_reported_not_crashed():
 
 
 def test_synth_normal_is_deterministic_and_normal():
-    L = _lib.lib()
+    L = _lib.testdata_lib()
     a = np.array([L.dh_synth_normal(7, i) for i in range(20000)])
     assert np.array_equal(a, [L.dh_synth_normal(7, i) for i in range(20000)])
     assert abs(a.mean()) < 0.03 and abs(a.std() - 1) < 0.03
@@ -84,7 +101,7 @@ def test_synth_normal_is_deterministic_and_normal():
 def test_synth_fp8_pages_round_like_torch(fmt):
     """The synthetic page encoder rounds to nearest even and saturates at 448,
     like torch's float8_e4m3fn conversion of the pre-clamped value."""
-    L = _lib.lib()
+    L = _lib.testdata_lib()
     hkv, d = 2, 64
     ids = np.array([3, 9], dtype=np.uint32)
     page_elems = 2 * hkv * 16 * d

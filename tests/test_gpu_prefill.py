@@ -88,19 +88,26 @@ def test_prefill_causal(backend, shape, fmt):
     _run(backend, hq, hkv, d, fmt[0], fmt[1], kv_len=[300, 17], q_len=[45, 17], chunk_pages=2, seed=1)
 
 
+@pytest.mark.parametrize("q_dtype", [_lib.DTYPE_BF16, _lib.DTYPE_F16], ids=["bf16q", "f16q"])
 @pytest.mark.parametrize("fmt", [_lib.KV_FP8_E4M3, _lib.KV_MXFP8], ids=["fp8", "mxfp8"])
 @pytest.mark.parametrize("d", [128, 256])
-def test_prefill_fp8(backend, fmt, d):
-    _run(backend, 16, 4, d, _lib.DTYPE_BF16, fmt, kv_len=[200, 40], q_len=[64, 40], chunk_pages=3, seed=d)
+def test_prefill_fp8(backend, fmt, d, q_dtype):
+    """FP8 / MXFP8 pools with bf16 or f16 queries (BatchPrefillConfig.dtype
+    0 = f16, 1 = bf16, flashinfer/batch_prefill.rs:23): the codes are
+    dequantised to the query's type in the kernel."""
+    _run(backend, 16, 4, d, q_dtype, fmt, kv_len=[200, 40], q_len=[64, 40], chunk_pages=3, seed=d + q_dtype)
+    _run(backend, 32, 8, d, q_dtype, fmt, kv_len=[700], q_len=[300], causal=False, seed=d + 7 * q_dtype,
+         gqa=_lib.GQA_INTERLEAVED)
 
 
+@pytest.mark.parametrize("q_dtype", [_lib.DTYPE_BF16, _lib.DTYPE_F16], ids=["bf16q", "f16q"])
 @pytest.mark.parametrize("fmt", [_lib.KV_FP8_E4M3, _lib.KV_MXFP8], ids=["fp8", "mxfp8"])
-def test_prefill_rejects_f16_queries_over_8bit_kv(backend, fmt):
-    """Decode takes f16 queries over FP8 / MXFP8 pools; prefill does not
-    (DH_EUNSUPPORTED at plan creation, before any launch)."""
+def test_prefill_rejects_8bit_kv_at_head_dim_64(backend, fmt, q_dtype):
+    """FP8 / MXFP8 pools at head_dim 64 have no prefill kernel
+    (DH_EUNSUPPORTED at plan creation, before any launch); decode takes them."""
     from dendrite_amd.backend import DhError
     with pytest.raises(DhError) as e:
-        _run(backend, 16, 4, 128, _lib.DTYPE_F16, fmt, kv_len=[40], q_len=[40])
+        _run(backend, 16, 4, 64, q_dtype, fmt, kv_len=[40], q_len=[40])
     assert e.value.status == _lib.DH_EUNSUPPORTED
 
 
