@@ -1025,11 +1025,34 @@ dh_status dh_decode_batch_static(dh_backend* be, const dh_pool* pool, const dh_p
 
 namespace {
 
+// Whether a CSR call looks for shared prefixes (group items need 16-bit
+// queries; the common-prefix pass keeps one LDS entry per sequence).
+bool csr_cascade(const dh_attn_config& c, uint32_t batch) {
+    return c.q_dtype != DH_DTYPE_F32 && batch >= 2 && batch <= dh::kCsrCascadeMaxBatch;
+}
+
+uint32_t csr_group_rows(const dh_attn_config& c) {
+    const bool fp8 = c.kv_format == DH_KV_FP8_E4M3 || c.kv_format == DH_KV_MXFP8;
+    return uint32_t(dh::group_rows(fp8, int(c.head_dim)));
+}
+
+// Group items a CSR call may emit: the planning kernel keeps them near 256
+// (one per CU) by its chunk choice, up to 32 chunks of 256 pages per group
+// and KV head (DH_MAX_SEQ_LEN); bounded by kCsrMaxGroupItems.
+uint32_t csr_group_cap(const dh_attn_config& c, uint32_t batch) {
+    if (!csr_cascade(c, batch)) return 0;
+    const uint64_t r = c.num_heads / c.num_kv_heads, gr = csr_group_rows(c);
+    const uint64_t cap = 256 + 32ull * c.num_kv_heads * ((uint64_t(batch) * r + gr - 1) / gr);
+    return uint32_t(std::min<uint64_t>(cap, dh::kCsrMaxGroupItems));
+}
+
 // Workspace of dh_decode_csr for `slots` partial-state slots, each section
 // 256-byte aligned: header, slot_ptr[B+1], seq_bad[B], seqslots[slots],
-// partial O [slots][Hq][D] (fp32 for f32 queries, else f16), log-sum-exps.
+// partial O [slots][Hq][D] (fp32 for f32 queries, else f16), log-sum-exps;
+// with a cascade also the common-prefix slices [B][kCsrLcpSlices], the skip
+// words [B] and the group items [gcap].
 struct CsrLayout {
-    size_t hdr, slot_ptr, seq_bad, seqslots, ws_o, ws_lse, total;
+    size_t hdr, slot_ptr, seq_bad, seqslots, ws_o, ws_lse, lcp, skip, gitems, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -1037,13 +1060,17 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 CsrLayout csr_layout(const dh_attn_config& c, uint32_t batch, uint64_t slots) {
     CsrLayout l;
     const size_t eb = c.q_dtype == DH_DTYPE_F32 ? 4 : 2;
+    const bool casc = csr_cascade(c, batch);
     l.hdr = 0;
     l.slot_ptr = align256(sizeof(dh::CsrHeader));
     l.seq_bad = l.slot_ptr + align256(size_t(batch + 1) * 4);
     l.seqslots = l.seq_bad + align256(size_t(batch) * 4);
     l.ws_o = l.seqslots + align256(slots * sizeof(dh::SeqSlot));
     l.ws_lse = l.ws_o + align256(slots * c.num_heads * c.head_dim * eb);
-    l.total = l.ws_lse + align256(slots * c.num_heads * sizeof(dh::PartialLse));
+    l.lcp = l.ws_lse + align256(slots * c.num_heads * sizeof(dh::PartialLse));
+    l.skip = l.lcp + (casc ? align256(size_t(batch) * dh::kCsrLcpSlices * 4) : 0);
+    l.gitems = l.skip + (casc ? align256(size_t(batch) * 4) : 0);
+    l.total = l.gitems + align256(size_t(csr_group_cap(c, batch)) * sizeof(dh::Item));
     return l;
 }
 
@@ -1054,7 +1081,7 @@ uint32_t csr_row_blocks(const dh_attn_config& c) {
 
 // Slots beyond the batch's own that a call uses at most (its grid covers
 // them; a larger workspace is not used past this).
-constexpr uint64_t kCsrMaxExtraSlots = 4096;
+constexpr uint64_t kCsrMaxExtraSlots = 4096, kCsrMaxCascadeSlots = 8192;
 constexpr uint32_t kCsrMaxBatch = 65536;
 
 }  // namespace
@@ -1068,7 +1095,10 @@ size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch, uint32_t
     const uint64_t need = (t + dh::kCsrMaxChunk - 1) / dh::kCsrMaxChunk;
     const uint64_t par = std::min((t + dh::kCsrMinChunk - 1) / dh::kCsrMinChunk,
                                   (2 * uint64_t(dh::kCsrWaveSlots) + per - 1) / per);
-    const uint64_t extra = std::min(kCsrMaxExtraSlots, std::max<uint64_t>(1, std::max(need, par)));
+    uint64_t extra = std::min(kCsrMaxExtraSlots, std::max<uint64_t>(1, std::max(need, par)));
+    // A cascade's group chunks take one slot per member: at most one per 8
+    // shared pages of each sequence, plus one per sequence for rounding.
+    if (csr_cascade(*cfg, batch)) extra += std::min(kCsrMaxCascadeSlots, (t + 7) / 8 + batch);
     return csr_layout(*cfg, batch, uint64_t(batch) + extra).total;
 }
 
@@ -1099,7 +1129,7 @@ dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_confi
     const size_t per_slot = sizeof(dh::SeqSlot) + size_t(c.num_heads) * sizeof(dh::PartialLse) +
                             size_t(c.num_heads) * c.head_dim * (c.q_dtype == DH_DTYPE_F32 ? 4 : 2);
     uint64_t slots = ws_bytes > one.total ? 1 + (ws_bytes - one.total) / per_slot : 0;
-    const uint64_t cap = uint64_t(batch) + kCsrMaxExtraSlots;
+    const uint64_t cap = uint64_t(batch) + kCsrMaxExtraSlots + (csr_cascade(c, batch) ? kCsrMaxCascadeSlots : 0);
     slots = std::min(slots, cap);
     // The estimate ignores the sections' alignment: settle on the exact count.
     while (slots < cap && csr_layout(c, batch, slots + 1).total <= ws_bytes) ++slots;
@@ -1125,6 +1155,16 @@ dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_confi
     const uint32_t nrb = csr_row_blocks(c);
     const uint32_t per_chunk = c.num_kv_heads * nrb;
 
+    const bool casc = csr_cascade(c, batch);
+    const uint32_t gcap = csr_group_cap(c, batch);
+    auto* lcp = reinterpret_cast<uint32_t*>(w + l.lcp);
+    auto* skip = reinterpret_cast<uint32_t*>(w + l.skip);
+    auto* gitems = reinterpret_cast<dh::Item*>(w + l.gitems);
+    hipError_t e = hipSuccess;
+    if (casc) {
+        e = hipError_t(dh::launch_csr_lcp(indptr, indices, batch, pool->num_pages, lcp, stream));
+        if (e != hipSuccess) return fail(DH_EHIP, "CSR common-prefix launch failed: %s", hipGetErrorString(e));
+    }
     dh::CsrPlanArgs p{};
     p.indptr = indptr;
     p.batch = batch;
@@ -1134,10 +1174,19 @@ dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_confi
     p.slot_ptr = slot_ptr;
     p.seq_bad = seq_bad;
     p.seqslots = seqslots;
-    hipError_t e = hipError_t(dh::launch_csr_plan(p, stream));
+    p.lcp = casc ? lcp : nullptr;
+    p.skip = skip;
+    p.gitems = gitems;
+    p.gcap = gcap;
+    p.hkv = c.num_kv_heads;
+    p.r = c.num_heads / c.num_kv_heads;
+    p.group_rows = csr_group_rows(c);
+    e = hipError_t(dh::launch_csr_plan(p, stream));
     if (e != hipSuccess) return fail(DH_EHIP, "CSR planning launch failed: %s", hipGetErrorString(e));
 
     dh::AttendArgs a{};
+    a.items = gitems;
+    a.csr_skip = casc ? skip : nullptr;
     a.pages = reinterpret_cast<const uint32_t*>(indices);
     a.seqslots = seqslots;
     a.q = q;
@@ -1159,11 +1208,13 @@ dh_status dh_decode_csr(dh_backend* be, const dh_pool* pool, const dh_attn_confi
     a.csr_hdr = reinterpret_cast<const uint32_t*>(hdr);
     a.seq_bad = seq_bad;
     a.csr_nrb = nrb;
-    // One wave per item, four per workgroup, over every slot the workspace
-    // holds; waves past the call's item count exit at once.
+    // The group items the planning kernel writes (at most gcap) take the
+    // first workgroups; then one wave per wave item, four per workgroup,
+    // over every slot the workspace holds.  Workgroups past the call's
+    // items exit at once.
     const uint64_t waves = slots * per_chunk;
-    e = hipError_t(dh::launch_attend(a, uint32_t((waves + dh::kWaves - 1) / dh::kWaves), c.q_dtype, c.kv_format,
-                                     c.head_dim, false, stream));
+    e = hipError_t(dh::launch_attend(a, uint32_t(gcap + (waves + dh::kWaves - 1) / dh::kWaves), c.q_dtype,
+                                     c.kv_format, c.head_dim, false, stream));
     if (e != hipSuccess) return fail(DH_EHIP, "attention launch failed: %s", hipGetErrorString(e));
 
     dh::MergeArgs m{};

@@ -177,22 +177,38 @@ __device__ __forceinline__ void row_target(const AttendArgs& a, const Item& it, 
     qh = a.gqa_tiled ? it.kv_head + j * a.hkv : it.kv_head * a.r + j;
 }
 
-// Item of wave `wave` in a workgroup past the group items (AttendArgs).
-__device__ __forceinline__ uint32_t wave_item_index(const AttendArgs& a, int wave) {
-    return a.n_group_items + (blockIdx.x - a.n_group_items) * kWaves + uint32_t(wave);
+// Group items of the launch: the plan's count, or on the CSR path what the
+// CSR planning kernel of this call wrote (its group items come first).
+__device__ __forceinline__ uint32_t group_item_count(const AttendArgs& a) {
+    return a.csr_hdr ? __builtin_amdgcn_readfirstlane(a.csr_hdr[4]) : a.n_group_items;
+}
+
+// Item of wave `wave` in a workgroup past the ng group items (AttendArgs):
+// on the plan path an index into the items (group items first), on the CSR
+// path the wave item's own number (csr_item).
+__device__ __forceinline__ uint32_t wave_item_index(const AttendArgs& a, int wave, uint32_t ng) {
+    return (a.csr_hdr ? 0u : ng) + (blockIdx.x - ng) * kWaves + uint32_t(wave);
 }
 
 // Wave items on the plan path: the plan's count; on the CSR path: what the
-// CSR planning kernel of this call wrote.
+// CSR planning kernel of this call wrote (its nodes' wave items, then one
+// per chunk of each sequence's own pages).
 __device__ __forceinline__ uint32_t wave_item_end(const AttendArgs& a) {
-    return a.csr_hdr ? __builtin_amdgcn_readfirstlane(a.csr_hdr[1]) : a.n_group_items + a.n_wave_items;
+    return a.csr_hdr ? __builtin_amdgcn_readfirstlane(a.csr_hdr[1]) + __builtin_amdgcn_readfirstlane(a.csr_hdr[6])
+                     : a.n_group_items + a.n_wave_items;
 }
+
+// Wave item idx of a CSR call: the cascade's node wave items (stored after
+// its ng group items in a.items), then the items derived from the tables.
+__device__ __forceinline__ Item csr_wave_item(const AttendArgs& a, uint32_t idx, uint32_t ng);
 
 // Wave item idx of a CSR call, derived from the tables: idx = (j * hkv +
 // kv_head) * nrb + row block; seqslots[j] names the j-th chunk in dispatch
-// order, chunk k of sequence b in slot slot_ptr[b] + k, pages
-// indptr[b] + k * chunk .. (the last chunk ends at b's last page).  seq_off
-// = j: the row's slot is read back from seqslots[j] (row_target).
+// order, chunk k of sequence b in slot slot_ptr[b] + G + k, pages
+// indptr[b] + L + k * chunk .. (the last chunk ends at b's last page), where
+// b's first L pages are read by group items into its first G slots (csr_skip;
+// L = G = 0 without a cascade).  seq_off = j: the row's slot is read back from
+// seqslots[j] (row_target).
 __device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
     const uint32_t nrb = a.csr_nrb, per = a.hkv * nrb;
     const uint32_t j = idx / per, rem = idx - j * per;
@@ -200,8 +216,9 @@ __device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
     const uint32_t b = __builtin_amdgcn_readfirstlane(a.seqslots[j].seq);
     const uint32_t slot = __builtin_amdgcn_readfirstlane(a.seqslots[j].slot);
     const uint32_t chunk = __builtin_amdgcn_readfirstlane(a.csr_hdr[0]);
-    const uint32_t k = slot - __builtin_amdgcn_readfirstlane(a.csr_slot_ptr[b]);
-    const uint32_t p0 = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b]));
+    const uint32_t skip = a.csr_skip ? __builtin_amdgcn_readfirstlane(a.csr_skip[b]) : 0u;
+    const uint32_t k = slot - __builtin_amdgcn_readfirstlane(a.csr_slot_ptr[b]) - (skip >> 16);
+    const uint32_t p0 = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b])) + (skip & 0xFFFFu);
     const uint32_t n = uint32_t(__builtin_amdgcn_readfirstlane(a.csr_indptr[b + 1])) - p0;
     Item it;
     it.page_off = p0 + k * chunk;
@@ -213,6 +230,11 @@ __device__ __forceinline__ Item csr_item(const AttendArgs& a, uint32_t idx) {
     it.flags = (k + 1) * chunk >= n ? kItemTail : 0u;
     it.tail_seq = b;
     return it;
+}
+
+__device__ __forceinline__ Item csr_wave_item(const AttendArgs& a, uint32_t idx, uint32_t ng) {
+    const uint32_t nw = __builtin_amdgcn_readfirstlane(a.csr_hdr[6]);
+    return idx < nw ? a.items[ng + idx] : csr_item(a, idx - nw);
 }
 
 // Valid tokens of page index i of an item.
@@ -2104,15 +2126,16 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attend16_kernel(AttendA
     // Wave index as a wave-uniform (scalar) value: page-list reads then go
     // through the scalar cache and never wait on the vector loads in flight.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (blockIdx.x < a.n_group_items) {
+    const uint32_t ng = group_item_count(a);
+    if (blockIdx.x < ng) {
         const Item it = a.items[blockIdx.x];
         if constexpr ((KVF == KVF_FP8 || KVF == KVF_MX) && D == 64) group_item<D, KVF, F16>(a, it, tid, wave, g, c);
         else if constexpr (KVF == KVF_FP8 || KVF == KVF_MX) group_item_dma8<D, KVF, F16, false>(a, it, tid, wave, g, c);
         else group_item_dma<D, F16, false>(a, it, tid, wave, g, c);
     } else {
-        const uint32_t idx = wave_item_index(a, wave);
+        const uint32_t idx = wave_item_index(a, wave, ng);
         if (idx < wave_item_end(a)) {
-            const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
+            const Item it = a.csr_hdr ? csr_wave_item(a, idx, ng) : a.items[idx];
             if (it.npages) wave_item<D, KVF, F16>(a, it, g, c);   // direct tasks pad with empty items
         }
         if (a.wave_direct) wave_task_merge<D, F16 ? 0u : 1u>(a, wave, tid & 63);
@@ -2241,9 +2264,9 @@ template <int D>
 __global__ __launch_bounds__(256) void attend32_kernel(AttendArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t idx = wave_item_index(a, wave);
+    const uint32_t idx = wave_item_index(a, wave, group_item_count(a));   // f32: no group items
     if (idx < wave_item_end(a)) {
-        const Item it = a.csr_hdr ? csr_item(a, idx) : a.items[idx];
+        const Item it = a.csr_hdr ? csr_wave_item(a, idx, 0) : a.items[idx];
         if (it.npages) attend32_item<D>(a, it, lane, g, c);   // direct tasks pad with empty items
     }
     if (a.wave_direct) wave_task_merge<D, 2u>(a, wave, lane);
@@ -2615,6 +2638,449 @@ __device__ __forceinline__ uint32_t csr_candidate(uint32_t i) {
 
 __device__ __forceinline__ uint32_t csr_cost(uint32_t pages) { return kCsrStartPairs + (pages + 1) / 2; }
 
+// Common prefix of adjacent sequences (CSR cascade): one wave per (boundary
+// b, slice s), b = 1 .. batch - 1, grid-strided.  The boundary's cap is one
+// page short of the shorter sequence (each sequence keeps its last page,
+// which alone may be partial); slice s covers positions s * kCsrLcpSlice ..
+// of it, read 64 ids a load, every load of the slice issued before the
+// first compare.  A sequence whose indptr entries are negative or decreasing
+// shares nothing.
+__global__ __launch_bounds__(256) void csr_lcp_kernel(const int32_t* indptr, const int32_t* indices,
+                                                      uint32_t batch, uint32_t page_limit, uint32_t* lcp) {
+    constexpr uint32_t U = kCsrLcpSlice / 64;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t nw = gridDim.x * kWaves, total = (batch - 1) * kCsrLcpSlices;
+    for (uint32_t w = blockIdx.x * kWaves + (threadIdx.x >> 6); w < total; w += nw) {
+        const uint32_t b = 1 + w / kCsrLcpSlices, s = w % kCsrLcpSlices;
+        const int32_t a0 = __builtin_amdgcn_readfirstlane(indptr[b - 1]);
+        const int32_t a1 = __builtin_amdgcn_readfirstlane(indptr[b]);
+        const int32_t b1 = __builtin_amdgcn_readfirstlane(indptr[b + 1]);
+        uint32_t cap = 0;
+        if (a0 >= 0 && a1 >= a0 && b1 >= a1) {
+            const uint32_t m = min(uint32_t(a1 - a0), uint32_t(b1 - a1));
+            cap = m ? min(m - 1, DH_MAX_SEQ_LEN / kPageSize - 1) : 0u;
+        }
+        const uint32_t lo = s * kCsrLcpSlice, hi = min(lo + kCsrLcpSlice, cap);
+        uint32_t first = cap, bad = 0xFFFFu;
+        if (lo < hi) {
+            int32_t x[U], y[U];
+            #pragma unroll
+            for (uint32_t j = 0; j < U; ++j) {
+                const uint32_t pos = lo + 64 * j + lane;
+                x[j] = pos < hi ? indices[uint32_t(a0) + pos] : 0;
+                y[j] = pos < hi ? indices[uint32_t(a1) + pos] : 0;
+            }
+            #pragma unroll
+            for (int j = int(U) - 1; j >= 0; --j) {   // the lowest sub-block's positions win
+                const uint32_t pos = lo + 64 * uint32_t(j) + lane;
+                const uint64_t ne = __ballot(pos < hi && x[j] != y[j]);
+                const uint64_t bd = __ballot(pos < hi && x[j] == y[j] && uint32_t(x[j]) >= page_limit);
+                if (ne) first = lo + 64 * uint32_t(j) + uint32_t(__builtin_ctzll(ne));
+                if (bd) bad = lo + 64 * uint32_t(j) + uint32_t(__builtin_ctzll(bd));
+            }
+            if (bad >= first) bad = 0xFFFFu;
+        }
+        if (lane == 0) lcp[b * kCsrLcpSlices + s] = first | (bad << 16);
+    }
+}
+
+// Inclusive max-scan of x over the workgroup in thread order; *tot receives
+// the maximum of all.  lds: NT / 64 words.
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t block_max_scan(uint32_t x, uint32_t* lds, uint32_t& tot) {
+    x = ~wave_scan_dpp<true>(~x);
+    if constexpr (NT == 64) {
+        tot = __builtin_amdgcn_readlane(x, 63);
+        return x;
+    } else {
+        constexpr uint32_t NW = NT / 64;
+        const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+        if (lane == 63) lds[wave] = x;
+        __syncthreads();
+        uint32_t before = 0;
+        tot = 0;
+        #pragma unroll
+        for (uint32_t w = 0; w < NW; ++w) {
+            const uint32_t v = lds[w];
+            before = w < wave ? max(before, v) : before;
+            tot = max(tot, v);
+        }
+        __syncthreads();
+        return max(x, before);
+    }
+}
+
+// The cascade of a CSR call (LDS): per sequence b (and boundary b, between
+// sequences b - 1 and b) and per node.  A node is a run of consecutive
+// sequences b0 .. b0 + cnt - 1 and the pages [pd, len) they share: their
+// common prefix is at least len pages and their parent node's is pd.  Nodes
+// nest as the shared prefixes of a fork tree do (the parent's run holds the
+// child's).  Node kinds: group items (kind 1, rows over 64, or over 16 with
+// more than 16 pages) or wave items of 16 rows (kind 0, chunks of
+// kCsrWaveChunk pages), as the host planner treats shared segments.
+constexpr uint32_t kCsrMaxLevels = 4, kCsrMaxNodes = 512, kCsrWaveChunk = 32, kCsrNoDepth = 0xFFFFFFFFu;
+struct CsrCascade {
+    uint32_t lcp[kCsrCascadeMaxBatch];     // common prefix of b - 1 and b (pages)
+    uint32_t bad[kCsrCascadeMaxBatch];     // first shared id outside the pool there (0xFFFF: none)
+    uint32_t pd[kCsrCascadeMaxBatch];      // depth of the deepest node holding b - 1 and b (kCsrNoDepth: none)
+    uint32_t head[kCsrCascadeMaxBatch];    // run head of b at the current level
+    uint32_t tmp[kCsrCascadeMaxBatch];     // scan scratch, later b's first slot
+    uint32_t acc[kCsrCascadeMaxBatch];     // at a head: members | 1 << 31 if poisoned
+    uint32_t mn[kCsrCascadeMaxBatch];      // at a head: shortest common prefix of its run
+    uint32_t skip[kCsrCascadeMaxBatch];    // skip word of b (AttendArgs::csr_skip)
+    uint32_t ip[kCsrCascadeMaxBatch];      // indptr[b]
+    uint32_t lv[kCsrMaxLevels][kCsrCascadeMaxBatch];   // node id + 1 of b at a level | slot offset << 16
+    uint32_t b0[kCsrMaxNodes], cnt[kCsrMaxNodes], npd[kCsrMaxNodes], len[kCsrMaxNodes];
+    uint32_t gc[kCsrMaxNodes], kind[kCsrMaxNodes], item0[kCsrMaxNodes], ss0[kCsrMaxNodes];
+    uint32_t nn;
+};
+
+// The cascade pass of the CSR planning kernel: nodes level by level from the
+// adjacent common prefixes.  At each level a boundary is internal when its
+// common prefix reaches kCsrMinShared pages past the depth of the deepest
+// node holding both its sequences; maximal runs of internal boundaries are
+// the level's nodes, each sharing down to the shortest prefix of its run.
+// Group items take chunks of `gchunk` pages: the smallest power of two from
+// 8 to 256 whose group items number at most 256 (one per CU), else 256.  A
+// node whose shared pages hold a page id outside the pool poisons its
+// members (s_bad[b] = 1).  When the items exceed gcap, or the slots leave
+// fewer than one per sequence for the rest, nothing is grouped.  Writes the
+// skip words (c.skip, p.skip), c.lv and the node records; returns the group
+// items, *n_wave the nodes' wave items, *gslots the slots of node chunks.
+// The nodes' share of the chip for the chunk choice of the sequences' own
+// pages: wave slots they hold, their cost (page pairs plus kCsrStartPairs
+// per item, times the waves of an item) and their largest item's cost.
+struct CsrNodeLoad {
+    uint32_t waves, cost, max_item;
+};
+
+template <uint32_t NT>
+__device__ uint32_t csr_cascade(const CsrPlanArgs& p, CsrCascade& c, uint32_t* s_bad, uint32_t* red,
+                                uint32_t& n_wave, uint32_t& gslots, uint32_t& gchunk, CsrNodeLoad& load) {
+    const uint32_t B = p.batch, tid = threadIdx.x;
+    // Every slice of a boundary loads at once (one memory round trip), and
+    // indptr[b] goes to LDS for the items' page offsets.
+    for (uint32_t b = tid; b < B; b += NT) {
+        uint32_t mn = 0, bd = 0xFFFFu, v[kCsrLcpSlices];
+        c.ip[b] = uint32_t(p.indptr[b]);
+        #pragma unroll
+        for (uint32_t s = 0; s < kCsrLcpSlices; ++s) v[s] = b > 0 ? p.lcp[b * kCsrLcpSlices + s] : 0u;
+        if (b > 0) {
+            mn = 0xFFFFu;
+            #pragma unroll
+            for (uint32_t s = 0; s < kCsrLcpSlices; ++s) {
+                mn = min(mn, v[s] & 0xFFFFu);
+                bd = min(bd, v[s] >> 16);
+            }
+        }
+        c.lcp[b] = mn;
+        c.bad[b] = bd;
+        c.pd[b] = b > 0 ? 0u : kCsrNoDepth;
+        c.skip[b] = 0u;
+        #pragma unroll
+        for (uint32_t l = 0; l < kCsrMaxLevels; ++l) c.lv[l][b] = 0u;
+    }
+    if (tid == 0) c.nn = 0;
+    __syncthreads();
+    auto internal = [&](uint32_t b) {
+        return b > 0 && c.pd[b] != kCsrNoDepth && c.lcp[b] >= c.pd[b] + kCsrMinShared;
+    };
+    // Each level in one pass over the sequences (in rounds of NT), by
+    // scans in thread order: b's run head is the max-scan of the non-internal
+    // indices; the run's shortest prefix and first bad id so far are the
+    // max-scans of (head << 16 | 0xFFFF - value), whose high half makes the
+    // maximum stay inside the run.  A run's last member holds its totals and
+    // records the node; its members read the node back from the head.
+    uint32_t levels = 0;
+    for (uint32_t lev = 0; lev < kCsrMaxLevels; ++lev) {
+        for (uint32_t b = tid; b < B; b += NT) c.acc[b] = 0u;
+        __syncthreads();
+        const uint32_t nn0 = c.nn;
+        uint32_t ch = 0, cm = 0, cb = 0, cn = 0;
+        for (uint32_t base = 0; base < B; base += NT) {
+            const uint32_t b = base + tid;
+            const bool valid = b < B, in = valid && internal(b);
+            uint32_t th, tm, tb;
+            const uint32_t h = max(block_max_scan<NT>(valid && !in ? b : 0u, red, th), ch);
+            const uint32_t mv = max(block_max_scan<NT>((h << 16) | (0xFFFFu - (in ? c.lcp[b] : 0xFFFFu)), red, tm), cm);
+            const uint32_t bv = max(block_max_scan<NT>((h << 16) | (0xFFFFu - (in ? c.bad[b] : 0xFFFFu)), red, tb), cb);
+            const bool last = valid && !(b + 1 < B && internal(b + 1));
+            const uint32_t cntb = b - h + 1;
+            // A run of fewer than 16 query rows is not worth a node: its
+            // sequences read the shared pages themselves (the second read
+            // mostly hits the caches), with fewer items and partial states.
+            const bool node = last && cntb >= 2u && cntb * p.r >= uint32_t(kWaveRows);
+            uint32_t x = node ? 1u : 0u, y = 0, tx, ty;
+            block_incl_scan2<NT>(x, y, red, tx, ty);
+            const uint32_t k = nn0 + cn + x - 1;
+            if (valid) c.head[b] = h;
+            if (node && k < kCsrMaxNodes) {
+                const uint32_t len = 0xFFFFu - (mv & 0xFFFFu), fb = 0xFFFFu - (bv & 0xFFFFu);
+                c.b0[k] = h;
+                c.cnt[k] = cntb;
+                c.npd[k] = c.pd[h + 1];            // h + 1 is internal: its pd is the run's
+                c.len[k] = len;
+                c.kind[k] = (lev << 1) | (fb < len ? 1u << 3 : 0u);   // level, poison; kind later
+                c.acc[h] = k + 1;
+                c.mn[h] = len;
+            }
+            ch = max(ch, th);
+            cm = max(cm, tm);
+            cb = max(cb, tb);
+            cn += tx;
+        }
+        __syncthreads();
+        if (cn == 0 || nn0 + cn > kCsrMaxNodes) break;   // no node, or too many: stop here
+        // Members take the node of their run; boundaries inside a node go one
+        // level deeper (their pd becomes the node's shared length).
+        for (uint32_t b = tid; b < B; b += NT) {
+            const uint32_t h = c.head[b], k1 = c.acc[h];
+            c.lv[lev][b] = k1;
+            c.tmp[b] = (k1 && internal(b)) ? c.mn[h] : kCsrNoDepth;
+        }
+        __syncthreads();
+        uint32_t deeper[1] = {0u};
+        for (uint32_t b = tid; b < B; b += NT) {
+            c.pd[b] = c.tmp[b];
+            deeper[0] |= (c.tmp[b] != kCsrNoDepth && c.lcp[b] >= c.tmp[b] + kCsrMinShared) ? 1u : 0u;
+        }
+        block_reduce<NT, false>(deeper, red);
+        if (tid == 0) c.nn = nn0 + cn;
+        __syncthreads();
+        levels = lev + 1;
+        if (!deeper[0]) break;   // no boundary reaches a deeper node
+    }
+    const uint32_t nn = c.nn;
+    // Kinds, and the items and slots of each chunk-size candidate.
+    constexpr uint32_t NC = 6;
+    uint32_t sums[2 * NC + 2] = {};
+    const uint32_t GR = p.group_rows;
+    for (uint32_t k = tid; k < nn; k += NT) {
+        const uint32_t rows = c.cnt[k] * p.r, pages = c.len[k] - c.npd[k];
+        const bool grp = rows > 64u || (rows > 16u && pages > 16u);
+        c.kind[k] |= grp ? 1u : 0u;
+        if (grp) {
+            const uint32_t rbk = (rows + GR - 1) / GR;
+            #pragma unroll
+            for (uint32_t i = 0; i < NC; ++i) {
+                const uint32_t g = (pages + (8u << i) - 1) >> (3 + i);
+                sums[i] += g * p.hkv * rbk;
+                sums[NC + i] += g * c.cnt[k];
+            }
+        } else {
+            const uint32_t g = (pages + kCsrWaveChunk - 1) / kCsrWaveChunk;
+            sums[2 * NC] += g * p.hkv * ((rows + kWaveRows - 1) / kWaveRows);
+            sums[2 * NC + 1] += g * c.cnt[k];
+        }
+    }
+    block_reduce<NT, false>(sums, red);
+    uint32_t pick = NC - 1, items_pick = sums[NC - 1], slots_pick = sums[2 * NC - 1];
+    #pragma unroll
+    for (int i = int(NC) - 1; i >= 0; --i) {
+        if (sums[i] <= 256u) {
+            pick = uint32_t(i);
+            items_pick = sums[i];
+            slots_pick = sums[NC + i];
+        }
+    }
+    const uint64_t need_slots = uint64_t(slots_pick) + sums[2 * NC + 1];
+    const bool on = nn > 0 && uint64_t(items_pick) + sums[2 * NC] <= p.gcap && need_slots + B <= p.slot_cap;
+    gchunk = on ? 8u << pick : 0u;
+    // Per node: chunks, first item (within its kind) and first seqslot; and
+    // the load its items put on the chip.
+    uint32_t ci = 0, cw = 0, cs = 0;
+    uint32_t ld[1] = {0u}, mx[1] = {~0u};
+    for (uint32_t base = 0; base < nn; base += NT) {
+        const uint32_t k = base + tid;
+        uint32_t gi = 0, wi = 0, ss = 0;
+        if (on && k < nn) {
+            const uint32_t rows = c.cnt[k] * p.r, pages = c.len[k] - c.npd[k];
+            const bool grp = c.kind[k] & 1u;
+            const uint32_t ch = grp ? gchunk : kCsrWaveChunk;
+            const uint32_t g = (pages + ch - 1) / ch, per = p.hkv * (grp ? (rows + GR - 1) / GR
+                                                                          : (rows + kWaveRows - 1) / kWaveRows);
+            c.gc[k] = g;
+            (grp ? gi : wi) = g * per;
+            ss = g * c.cnt[k];
+            const uint32_t w = grp ? uint32_t(kWaves) : 1u;
+            ld[0] += ((g - 1) * csr_cost(ch) + csr_cost(pages - (g - 1) * ch)) * per * w;
+            mx[0] = min(mx[0], ~csr_cost(min(ch, pages)));
+        }
+        uint32_t x = gi, y = wi, tx, ty;
+        block_incl_scan2<NT>(x, y, red, tx, ty);
+        uint32_t z = ss, zz = 0, tz, tzz;
+        block_incl_scan2<NT>(z, zz, red, tz, tzz);
+        if (on && k < nn) {
+            c.item0[k] = (c.kind[k] & 1u) ? ci + x - gi : cw + y - wi;
+            c.ss0[k] = cs + z - ss;
+        }
+        ci += tx;
+        cw += ty;
+        cs += tz;
+    }
+    block_reduce<NT, false>(ld, red);
+    block_reduce<NT, true>(mx, red);
+    load.waves = on ? ci * kWaves + cw : 0u;
+    load.cost = on ? ld[0] : 0u;
+    load.max_item = on && mx[0] != ~0u ? ~mx[0] : 0u;
+    __syncthreads();
+    // Per sequence: shared pages (its deepest node's), node chunks and the
+    // slot offset of each level's chunks; poisoned if any node of it is.
+    for (uint32_t b = tid; b < B; b += NT) {
+        uint32_t depth = 0, chunks = 0;
+        bool poison = false;
+        for (uint32_t l = 0; l < levels; ++l) {
+            const uint32_t k1 = c.lv[l][b] & 0xFFFFu;
+            if (!on || !k1) continue;
+            const uint32_t k = k1 - 1;
+            c.lv[l][b] = k1 | (chunks << 16);
+            chunks += c.gc[k];
+            depth = c.len[k];
+            poison |= (c.kind[k] >> 3) & 1u;
+        }
+        const uint32_t w = depth ? depth | (chunks << 16) : 0u;
+        c.skip[b] = w;
+        p.skip[b] = w;
+        s_bad[b] = poison ? 1u : 0u;
+    }
+    __syncthreads();
+    n_wave = on ? cw : 0u;
+    gslots = on ? cs : 0u;
+    if (!on && tid == 0) c.nn = 0;
+    __syncthreads();
+    return on ? ci : 0u;
+}
+
+// Items and seqslot entries of the cascade's nodes, one wave per node
+// (first slots of the sequences in c.tmp; seqslot entries from n_chunks on,
+// after the wave items' chunks).  Group items of a node cover unit u =
+// chunk * hkv + KV head and row block rb; units are taken eight at a time,
+// each with all its row blocks eight items apart, so the items reading the
+// same pages run on the same XCD (workgroup i runs on XCD i mod 8) and share
+// its L2.  Node wave items follow the group items in p.gitems.
+// Item i of a cascade node (CSR path): a group item (kind bit 0) of unit u
+// = chunk * hkv + KV head and row block rb, units eight at a time with
+// their row blocks eight items apart (items reading the same pages on one
+// XCD, workgroup i running on XCD i mod 8), or a wave item of 16 rows.
+__device__ __forceinline__ void csr_node_item(const CsrPlanArgs& p, uint32_t i, uint32_t b0, uint32_t cnt,
+                                                       uint32_t pd, uint32_t len, uint32_t g, uint32_t kind,
+                                                       uint32_t item0, uint32_t ss0, uint32_t p0, uint32_t n_chunks,
+                                                       uint32_t n_group, uint32_t gchunk) {
+    const uint32_t rows = cnt * p.r, GR = p.group_rows;
+    Item it;
+    if (kind & 1u) {
+        const uint32_t units = g * p.hkv, rbk = (rows + GR - 1) / GR;
+        const uint32_t blk = i / (8 * rbk), within = i - blk * 8 * rbk;
+        const uint32_t m = min(8u, units - blk * 8), rb = within / m, u = blk * 8 + within - rb * m;
+        const uint32_t chk = u / p.hkv;
+        it.page_off = p0 + pd + chk * gchunk;
+        it.npages = min(gchunk, len - pd - chk * gchunk);
+        it.seq_off = n_chunks + ss0 + chk * cnt;
+        it.row_begin = rb * GR;
+        it.nrows = min(GR, rows - rb * GR);
+        it.kv_head = u - chk * p.hkv;
+    } else {
+        const uint32_t nrb = (rows + kWaveRows - 1) / kWaveRows;
+        const uint32_t u = i / nrb, rb = i - u * nrb, chk = u / p.hkv;
+        it.page_off = p0 + pd + chk * kCsrWaveChunk;
+        it.npages = min(kCsrWaveChunk, len - pd - chk * kCsrWaveChunk);
+        it.seq_off = n_chunks + ss0 + chk * cnt;
+        it.row_begin = rb * kWaveRows;
+        it.nrows = min(uint32_t(kWaveRows), rows - rb * kWaveRows);
+        it.kv_head = u - chk * p.hkv;
+    }
+    it.flags = 0u;
+    it.tail_seq = b0;
+    p.gitems[((kind & 1u) ? 0u : n_group) + item0 + i] = it;
+}
+
+template <uint32_t NT>
+__device__ void csr_cascade_emit(const CsrPlanArgs& p, const CsrCascade& c, uint32_t n_chunks, uint32_t n_group,
+                                 uint32_t gchunk) {
+    constexpr uint32_t NW = NT / 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, GR = p.group_rows;
+    // Seqslots, one thread per sequence: for each node of it (one a level),
+    // its slot of every chunk (its first slot, the chunks of its shallower
+    // nodes, then the chunk's index) at entry ss0 + chunk * cnt + member.
+    for (uint32_t b = tid; b < p.batch; b += NT) {
+        #pragma unroll
+        for (uint32_t l = 0; l < kCsrMaxLevels; ++l) {
+            const uint32_t w = c.lv[l][b], k1 = w & 0xFFFFu;
+            if (!k1) continue;
+            const uint32_t k = k1 - 1, cnt = c.cnt[k], g = c.gc[k];
+            const uint32_t s0 = c.tmp[b] + (w >> 16);
+            SeqSlot* dst = p.seqslots + n_chunks + c.ss0[k] + (b - c.b0[k]);
+            for (uint32_t chk = 0; chk < g; ++chk) dst[chk * cnt] = SeqSlot{b, s0 + chk};
+        }
+    }
+    // Items.  A node with at most 64 items is written by one thread alone
+    // (most nodes of a tree are small, and a thread per node keeps them in
+    // parallel); a larger one by a whole wave, from a list of them.
+    __shared__ uint32_t s_big[kCsrMaxNodes + 1];
+    if (tid == 0) s_big[kCsrMaxNodes] = 0u;
+    __syncthreads();
+    auto n_items = [&](uint32_t k) {
+        const uint32_t rows = c.cnt[k] * p.r;
+        return c.gc[k] * p.hkv * ((c.kind[k] & 1u) ? (rows + GR - 1) / GR : (rows + kWaveRows - 1) / kWaveRows);
+    };
+    for (uint32_t k = tid; k < c.nn; k += NT) {
+        const uint32_t n = n_items(k);
+        if (n > 64u) {
+            s_big[atomicAdd(&s_big[kCsrMaxNodes], 1u)] = k;
+            continue;
+        }
+        const uint32_t b0 = c.b0[k];
+        const uint32_t cnt = c.cnt[k], pd = c.npd[k], len = c.len[k], g = c.gc[k], kind = c.kind[k];
+        const uint32_t item0 = c.item0[k], ss0 = c.ss0[k], p0 = c.ip[b0];
+        // The order of csr_node_item, walked with counters instead of
+        // divisions: units (chunk, KV head) eight at a time, then row
+        // blocks, then the units of the eight (group items); units, then
+        // row blocks (wave items).
+        const uint32_t rows = cnt * p.r, grp = kind & 1u;
+        const uint32_t rbk = grp ? (rows + GR - 1) / GR : (rows + kWaveRows - 1) / kWaveRows;
+        const uint32_t RR = grp ? GR : uint32_t(kWaveRows), ch = grp ? gchunk : kCsrWaveChunk;
+        const uint32_t units = g * p.hkv, step = grp ? 8u : 1u;
+        Item* out = p.gitems + (grp ? 0u : n_group) + item0;
+        uint32_t chk0 = 0, h0 = 0;                 // unit u0 = chk0 * hkv + h0
+        for (uint32_t u0 = 0; u0 < units; u0 += step) {
+            const uint32_t m = min(step, units - u0);
+            for (uint32_t rb = 0; rb < rbk; ++rb) {
+                uint32_t chk = chk0, h = h0;
+                for (uint32_t uu = 0; uu < m; ++uu) {
+                    Item it;
+                    it.page_off = p0 + pd + chk * ch;
+                    it.npages = min(ch, len - pd - chk * ch);
+                    it.seq_off = n_chunks + ss0 + chk * cnt;
+                    it.row_begin = rb * RR;
+                    it.nrows = min(RR, rows - rb * RR);
+                    it.kv_head = h;
+                    it.flags = 0u;
+                    it.tail_seq = b0;
+                    *out++ = it;
+                    if (++h == p.hkv) {
+                        h = 0;
+                        ++chk;
+                    }
+                }
+            }
+            for (uint32_t uu = 0; uu < m; ++uu) {
+                if (++h0 == p.hkv) {
+                    h0 = 0;
+                    ++chk0;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t t = wave; t < s_big[kCsrMaxNodes]; t += NW) {
+        const uint32_t k = s_big[t], n = n_items(k), b0 = c.b0[k];
+        const uint32_t cnt = c.cnt[k], pd = c.npd[k], len = c.len[k], g = c.gc[k], kind = c.kind[k];
+        const uint32_t item0 = c.item0[k], ss0 = c.ss0[k], p0 = c.ip[b0];
+        for (uint32_t i = lane; i < n; i += 64)
+            csr_node_item(p, i, b0, cnt, pd, len, g, kind, item0, ss0, p0, n_chunks, n_group, gchunk);
+    }
+}
+
 // Work decomposition of one dh_decode_csr call, on the device: sequence b's
 // pages indptr[b] .. indptr[b+1] split into chunks of `chunk` pages (the last
 // one shorter), chunk k of b in partial-state slot slot_ptr[b] + k.
@@ -2646,16 +3112,30 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     constexpr uint32_t KC = kCsrFixedCandidates, KM = KC + 1;
     __shared__ uint32_t red[(NT / 64) * 2 * KM];
     __shared__ uint32_t s_tail[kCsrMaxChunk];    // last chunks of each size, then their next position
+    // Cascade: its nodes and per-sequence state; members of poisoned nodes.
+    __shared__ CsrCascade cc;
+    __shared__ uint32_t s_bad[kCsrCascadeMaxBatch];
     const uint32_t tid = threadIdx.x;
     constexpr uint32_t kMaxSeqPages = DH_MAX_SEQ_LEN / kPageSize;
     const uint32_t iters = (p.batch + NT - 1) / NT;
+    // Shared prefixes of consecutive sequences first (nodes read by group or
+    // multi-sequence wave items): each sequence's own wave items then cover
+    // only the pages past its deepest node's.
+    const bool casc = p.lcp != nullptr && p.batch >= 2 && p.batch <= kCsrCascadeMaxBatch;
+    uint32_t n_gitems = 0, n_nwave = 0, gslots = 0, gchunk = 0;
+    CsrNodeLoad nload{0u, 0u, 0u};
+    if (casc) n_gitems = csr_cascade<NT>(p, cc, s_bad, red, n_nwave, gslots, gchunk, nload);
+    const bool grouped = gslots > 0;
     auto load = [&](uint32_t b, bool& ok) -> uint32_t {
         ok = false;
         if (b >= p.batch) return 0u;
         const int32_t p0 = p.indptr[b], p1 = p.indptr[b + 1];
         ok = p0 >= 0 && p1 >= p0 && uint32_t(p1 - p0) <= kMaxSeqPages;
-        return ok ? uint32_t(p1 - p0) : 0u;
+        if (!ok) return 0u;
+        return uint32_t(p1 - p0) - (grouped ? (cc.skip[b] & 0xFFFFu) : 0u);
     };
+    // Slots the wave items' chunks may take.
+    const uint32_t cap_s = p.slot_cap - gslots;
     constexpr uint32_t R = csr_reg_seqs(NT);
     uint32_t nr[R], okr = 0;
     #pragma unroll
@@ -2733,13 +3213,14 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     block_reduce<NT, true>(mins, red, active);
 
     // Chunks that leave a row more than kCsrMaxStates partial states (the
-    // merge kernel's vector path) rank after every other fitting one.
+    // merge kernel's vector path) rank after every other fitting one.  The
+    // cascade's node items (nload) hold wave slots and add their cost.
     auto end_of = [&](uint32_t c, uint32_t cnt, uint32_t cost, uint32_t mn) -> uint64_t {
-        if (cnt > p.slot_cap) return ~uint64_t(0);
-        const uint64_t S = kCsrWaveSlots, mx = csr_cost(min(c, maxn));
-        const uint64_t e = uint64_t(cnt) * p.per_chunk <= S
+        if (cnt > cap_s) return ~uint64_t(0);
+        const uint64_t S = kCsrWaveSlots, mx = max(csr_cost(min(c, maxn)), nload.max_item);
+        const uint64_t e = uint64_t(cnt) * p.per_chunk + nload.waves <= S
                                ? mx * S
-                               : max(mx * S, uint64_t(cost) * p.per_chunk + uint64_t(mn) * S);
+                               : max(mx * S, uint64_t(cost) * p.per_chunk + nload.cost + uint64_t(mn) * S);
         return c < need ? e | (uint64_t(1) << 62) : e;     // more than kCsrMaxStates chunks of maxn pages
     };
     uint32_t chunk = kCsrMaxChunk, n_chunks = sums[KC - 1];
@@ -2755,7 +3236,7 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
             n_chunks = sums[i];
         }
     }
-    const bool overflow = n_chunks > p.slot_cap;
+    const bool overflow = n_chunks > cap_s;
 
     // Pass 3: last chunks of each size; those of size t take the positions
     // n_chunks - (last chunks of size <= t) onwards, so the longest follow
@@ -2780,19 +3261,25 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     // Pass 4: each sequence's first slot (prefix sum of the chunk counts)
     // and its chunks' positions: full chunks after the full chunks of the
     // sequences before it, its last chunk from its size's range.
-    uint32_t carry = 0, carry_t = 0;
+    // With a cascade, a sequence's slots are its group chunks' (one per
+    // chunk of its group's shared pages) and then its wave items' chunks.
+    uint32_t carry = 0, carry_t = 0, carry_g = 0;
     each([&](uint32_t b, uint32_t n, bool ok) {
         const uint32_t full = n / chunk, t = n - full * chunk, has_t = t ? 1u : 0u, cnt = full + has_t;
-        uint32_t x = cnt, y = has_t, tx, ty;
+        const uint32_t gcb = (grouped && b < p.batch) ? cc.skip[b] >> 16 : 0u;
+        uint32_t x = cnt + gcb, y = has_t, tx, ty;
         block_incl_scan2<NT>(x, y, red, tx, ty);
-        const uint32_t first = carry + x - cnt;
-        const uint32_t fpos = first - (carry_t + y - has_t);
+        uint32_t xg = gcb, yg = 0, txg = 0, tyg;
+        if (grouped) block_incl_scan2<NT>(xg, yg, red, txg, tyg);
+        const uint32_t first = carry + x - cnt - gcb;
+        const uint32_t fpos = first - (carry_g + xg - gcb) - (carry_t + y - has_t);
         if (b < p.batch) {
             p.slot_ptr[b] = first;
-            p.seq_bad[b] = (ok && !overflow) ? 0u : 1u;
+            p.seq_bad[b] = (ok && !overflow && !(grouped && s_bad[b])) ? 0u : 1u;
+            if (grouped) cc.tmp[b] = first;
             if (!overflow && t) {
                 const uint32_t pos = atomicAdd(&s_tail[t], 1u);
-                if (pos < p.slot_cap) p.seqslots[pos] = SeqSlot{b, first + full};
+                if (pos < p.slot_cap) p.seqslots[pos] = SeqSlot{b, first + gcb + full};
             }
         }
         // Full chunks: each lane its own sequence's, or, in the one-wave
@@ -2804,22 +3291,35 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
         if (!overflow && by_wave) {
             for (uint32_t sq = 0; sq < p.batch; ++sq) {
                 const uint32_t fs = __builtin_amdgcn_readlane(full, sq), ps = __builtin_amdgcn_readlane(fpos, sq);
-                const uint32_t ss = __builtin_amdgcn_readlane(first, sq);
+                const uint32_t ss = __builtin_amdgcn_readlane(first + gcb, sq);
                 for (uint32_t k = tid; k < fs && ps + k < p.slot_cap; k += kCsrSmallThreads)
                     p.seqslots[ps + k] = SeqSlot{sq, ss + k};
             }
         } else if (!overflow && b < p.batch) {
-            for (uint32_t k = 0; k < full && fpos + k < p.slot_cap; ++k) p.seqslots[fpos + k] = SeqSlot{b, first + k};
+            for (uint32_t k = 0; k < full && fpos + k < p.slot_cap; ++k)
+                p.seqslots[fpos + k] = SeqSlot{b, first + gcb + k};
         }
         carry += tx;
         carry_t += ty;
+        carry_g += txg;
     });
+    // The nodes' items and seqslots (entries n_chunks .. n_chunks + gslots,
+    // after the wave items' chunks in dispatch order).
+    const bool emit = grouped && !overflow;
+    if (emit) {
+        __syncthreads();   // first slots (cc.tmp) of every sequence
+        csr_cascade_emit<NT>(p, cc, n_chunks, n_gitems, gchunk);
+    }
     if (tid == 0) {
-        p.slot_ptr[p.batch] = overflow ? 0u : n_chunks;
+        const uint32_t slots = n_chunks + gslots;
+        p.slot_ptr[p.batch] = overflow ? 0u : slots;
         p.hdr->chunk = chunk;
         p.hdr->n_items = overflow ? 0u : n_chunks * p.per_chunk;
         p.hdr->overflow = overflow ? 1u : 0u;
-        p.hdr->n_chunks = n_chunks;
+        p.hdr->n_chunks = slots;
+        p.hdr->n_group = emit ? n_gitems : 0u;
+        p.hdr->group_chunk = gchunk;
+        p.hdr->n_node_waves = emit ? n_nwave : 0u;
     }
 }
 
@@ -2996,6 +3496,17 @@ int launch_attend(const AttendArgs& a, uint32_t n_items, uint32_t q_dtype, uint3
         case 256: return launch_attend_d<256>(a, n_items, q_dtype, kvf, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+int launch_csr_lcp(const int32_t* indptr, const int32_t* indices, uint32_t batch, uint32_t page_limit,
+                   uint32_t* lcp, void* stream) {
+    if (batch < 2) return hipSuccess;
+    const uint64_t waves = uint64_t(batch - 1) * kCsrLcpSlices;
+    const uint64_t want = (waves + kWaves - 1) / kWaves;
+    const uint32_t blocks = uint32_t(want < 1024 ? want : 1024);
+    hipLaunchKernelGGL(csr_lcp_kernel, dim3(blocks), dim3(kWaves * 64), 0, reinterpret_cast<hipStream_t>(stream),
+                       indptr, indices, batch, page_limit, lcp);
+    return hipGetLastError();
 }
 
 int launch_csr_plan(const CsrPlanArgs& p, void* stream) {

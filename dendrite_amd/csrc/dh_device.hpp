@@ -127,6 +127,10 @@ struct AttendArgs {
     const uint32_t* csr_hdr;      // CsrHeader
     uint32_t* seq_bad;            // [B] set to 1 for a sequence with a bad page id
     uint32_t csr_nrb;             // row blocks of 16 per (chunk, kv head)
+    // Cascade on the CSR path: per sequence, its leading pages read by group
+    // items (bits 0..15) and the partial-state slots those take (bits
+    // 16..31); its wave items cover the rest.  Null: no cascade.
+    const uint32_t* csr_skip;
     // Direct decode plans: each wave task's items are the chunks of one
     // (sequence, KV head, row block); the workgroup merges its rows over the
     // sequence's slots (slot_ptr) into out itself.  0 / null otherwise.
@@ -143,11 +147,27 @@ struct AttendArgs {
 // What the CSR planning kernel leaves in the workspace for the attention
 // and merge kernels of the same call.
 struct CsrHeader {
-    uint32_t chunk;        // pages per chunk
+    uint32_t chunk;        // pages per chunk of the wave items
     uint32_t n_items;      // wave items (0 when the tables exceed the workspace)
     uint32_t overflow;     // 1: more chunks than the workspace holds
     uint32_t n_chunks;     // partial-state slots used
+    uint32_t n_group;      // group items (each a shared prefix's chunk, read once), first in the grid
+    uint32_t group_chunk;  // pages per chunk of the group items
+    uint32_t n_node_waves; // wave items of shared prefixes with few rows (items after the group items)
+    uint32_t pad;
 };
+
+// Common-prefix scan of adjacent sequences (csr_lcp_kernel): boundary b
+// (sequences b - 1 and b) is cut into kCsrLcpSlices slices of
+// kCsrLcpSlice positions; each slice records its first mismatching position
+// (or the boundary's cap, one page short of the shorter sequence, when none)
+// in bits 0..15 and its first page id outside the pool before that in bits
+// 16..31 (0xFFFF: none).  The common prefix is the minimum over the slices.
+constexpr uint32_t kCsrLcpSlices = 16, kCsrLcpSlice = 512;
+// Batches the CSR cascade is found for (one LDS entry per sequence), the
+// pages a shared prefix must add to its parent's to form a node, and the
+// node items (group and wave) a call may emit at most.
+constexpr uint32_t kCsrCascadeMaxBatch = 512, kCsrMinShared = 8, kCsrMaxGroupItems = 4096;
 
 // Inputs of the CSR planning kernel (one workgroup).
 struct CsrPlanArgs {
@@ -159,6 +179,15 @@ struct CsrPlanArgs {
     uint32_t* slot_ptr;      // [B+1]
     uint32_t* seq_bad;       // [B]
     SeqSlot* seqslots;       // [slot_cap]
+    // Cascade (null lcp: none): the common-prefix slices of csr_lcp_kernel,
+    // the per-sequence skip words (AttendArgs::csr_skip) and the node items
+    // written here (group items, then wave items), at most gcap of them;
+    // group rows per item and the head shape they are cut by.
+    const uint32_t* lcp;     // [B][kCsrLcpSlices]
+    uint32_t* skip;          // [B]
+    Item* gitems;            // [gcap]
+    uint32_t gcap;
+    uint32_t hkv, r, group_rows;
 };
 
 struct MergeArgs {
@@ -211,6 +240,8 @@ int launch_gather(const uint8_t* kv, const uint32_t* pages, uint32_t n_pages, ui
                   void* stream);
 bool attend_supported(uint32_t q_dtype, uint32_t kv_format, uint32_t head_dim);
 int launch_csr_plan(const CsrPlanArgs& p, void* stream);
+int launch_csr_lcp(const int32_t* indptr, const int32_t* indices, uint32_t batch, uint32_t page_limit,
+                   uint32_t* lcp, void* stream);
 // Wave slots of the chip the CSR path schedules against (256 CUs x two
 // workgroups x four waves), and its chunk sizes: 1 page up to what a wave
 // item's page-id registers hold.

@@ -415,8 +415,9 @@ dh_status dh_decode_batch_static(dh_backend* backend, const dh_pool* pool, const
  * tables hold at most max_total_pages entries together (indptr[batch] -
  * indptr[0] <= max_total_pages).  The size grows with batch_size and with
  * max_total_pages up to a cap (about two waves per wave slot of the chip,
- * 4 096 work items, in partial states), so a workspace sized for a long
- * context serves every shorter one.  Replaces
+ * 4 096 work items, in partial states, plus room for the shared prefixes'
+ * chunks when the call may find them: one per 8 pages, at most 8 192), so
+ * a workspace sized for a long context serves every shorter one.  Replaces
  * BatchDecodeKernel::workspace_size (flashinfer/batch_decode.rs:56-73). */
 size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch_size, uint32_t max_total_pages);
 
@@ -435,13 +436,23 @@ size_t dh_csr_workspace_size(const dh_attn_config* cfg, uint32_t batch_size, uin
  *                   sequences' outputs are zeros and no page outside the
  *                   pool is read) or DH_ENOMEM (the tables need more work
  *                   items than the workspace holds: every output is zeros).
- * Every sequence is split into chunks of one page count (the last chunk
- * shorter), chosen on the device from the tables for the earliest estimated
- * end over the chip's wave slots, 1 to 256 pages.  Each chunk is attended
- * by one wave and the chunks are merged by log-sum-exp: a flat batch,
- * without the shared-prefix reuse of a cascade plan.  Host checks (returned synchronously): cfg and
- * pool agree, the pointers are device memory, the workspace holds at least
- * batch + 1 chunks.  Three kernels on `stream`; allocates nothing. */
+ * Shared prefixes of consecutive sequences (what TreeState::fork
+ * produces, tree/state.rs:49-84) are read once, as CascadeAttention
+ * promises (flashinfer/cascade.rs:22-26): a first kernel compares every
+ * pair of adjacent page lists; the planning kernel nests the common
+ * prefixes into nodes (up to four levels, each adding at least 8 pages to
+ * its parent's, runs of at least 16 query rows, batches of 2 to 512
+ * sequences, 16-bit queries) whose pages are read once per KV head by
+ * shared-prefix MFMA items (or multi-sequence wave items for short runs).
+ * Every sequence's remaining pages are split into chunks of one page
+ * count (the last chunk shorter), chosen on the device from the tables
+ * for the earliest estimated end over the chip's wave slots, 1 to 256
+ * pages; all partial states are merged by log-sum-exp.  A page id outside
+ * the pool in a node's shared pages zeros every member.  Host checks
+ * (returned synchronously): cfg and pool agree, the pointers are device
+ * memory, the workspace holds at least batch + 1 chunks.  Four kernels on
+ * `stream` (three without a cascade: f32 queries, one sequence, or more
+ * than 512); allocates nothing. */
 dh_status dh_decode_csr(dh_backend* backend, const dh_pool* pool, const dh_attn_config* cfg,
                         uint32_t batch_size, const void* q, const int32_t* indices,
                         const int32_t* indptr, const int32_t* last_page_len, void* out,

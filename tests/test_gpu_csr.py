@@ -3,7 +3,12 @@ the device on every call (BatchDecodeKernel::run's contract,
 crates/dendrite-ffi/src/flashinfer/batch_decode.rs:86-95), against the CPU
 oracle on identical inputs, plus its error reporting: bad page ids and
 indptr entries (status DH_EINVAL, zeros for those sequences, no read outside
-the pool) and tables larger than the workspace (DH_ENOMEM, zeros).
+the pool) and tables larger than the workspace (DH_ENOMEM, zeros).  Shared
+prefixes of consecutive sequences (what TreeState::fork produces) are read
+once per KV head by group items (CascadeAttention's promise,
+crates/dendrite-ffi/src/flashinfer/cascade.rs:22-26): the call's header
+records how many, and the tests below check both the grouping and the
+results.
 Tolerances as in test_gpu_decode (f32 1e-4; 16-bit / FP8 2e-2 beyond the
 output dtype's rounding)."""
 import numpy as np
@@ -58,6 +63,12 @@ class CsrRun:
         return oracle.decode(pv, self.q_raw, w.q_dtype, w.hq, self.cfg.scale, w.gqa_mapping,
                              w.indptr if indptr is None else indptr, w.indices if indices is None else indices,
                              w.last_page_len if lpl is None else lpl, seqs=seqs)
+
+
+def header(run):
+    """The CSR call's header in the workspace: chunk, wave items, overflow,
+    slots, group items, group chunk, the nodes' wave items."""
+    return [int(x) for x in run.ws[:28].view(dtype=__import__("torch").int32).cpu()]
 
 
 def _check(run, got, ref, name):
@@ -130,14 +141,118 @@ def test_chunk_choice_shapes(backend, case):
     _check(run, got, run.reference(), case)
 
 
-def test_c3_full_flat(backend):
-    """The headline tree read flat from device tables: every leaf's 536
-    pages, all 64 leaves against the oracle."""
+def test_c3_full(backend):
+    """The headline tree from device tables, all 64 leaves against the
+    oracle: the 512-page root is one group's shared pages (read once per KV
+    head and 128-row block: 16 chunks x 8 heads x 2 blocks = 256 group
+    items), each leaf's other 24 pages go to wave items."""
     w = workloads.c3()
     run = CsrRun(w, backend)
     got, st = run.run()
     assert st == _lib.DH_OK
+    h = header(run)
+    print(f"[case] csr c3 header {h}", flush=True)
+    # root: 256 group items of 32 pages; the 4 level-1 runs (64 rows, 8
+    # pages) and 16 level-2 runs (16 rows): wave items of 16 rows, 4 x 8 x 4
+    # + 16 x 8 x 1; each leaf's last 8 pages its own
+    assert h[4] == 256 and h[5] == 32 and h[6] == 256
     _check(run, got, run.reference(), "c3 full")
+
+
+def _grouped(run):
+    """Items reading shared prefixes once: group items and nodes' wave items."""
+    h = header(run)
+    return h[4] + h[6]
+
+
+def test_cascade_groups(backend):
+    """Nodes of consecutive sequences: a common prefix of 8 pages or more
+    makes one, 7 does not; a sequence that is its successor's prefix shares
+    all but its last page; sequences that share a prefix but are not
+    adjacent are read flat; duplicates share all but their last page; a node
+    of 40 sequences x 8 heads of one KV head spans three 128-row blocks.
+    Nodes of 16 rows are read by wave items, larger ones by group items."""
+    import torch
+    rng = np.random.default_rng(5)
+    perm = iter(rng.permutation(4096).tolist())
+    take = lambda n: [next(perm) for _ in range(n)]  # noqa: E731
+    p20, p7, p30 = take(20), take(7), take(30)
+    tables = []
+    tables += [p20 + take(3) for _ in range(3)]             # group of 3, 20 shared pages
+    tables += [p7 + take(2) for _ in range(2)]              # 7 shared: no group
+    par = take(12)
+    tables += [par, par + take(4)]                          # prefix: 11 shared pages
+    x = take(9)
+    tables += [x + take(2), take(5), x + take(3)]           # not adjacent: flat
+    d = take(10)
+    tables += [d, list(d)]                                  # duplicates: 9 shared
+    tables += [p30 + take(1 + i % 3) for i in range(40)]    # 40 members
+    lpl = rng.integers(1, 17, len(tables)).astype(np.int32)
+    w = workloads.custom(tables, 8, 1, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 4096, last_page_len=lpl)
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    h = header(run)
+    print(f"[case] csr groups header {h}", flush=True)
+    # group items, chunk 8 (items at most 256): 3 and 4 chunks of the 20- and
+    # 30-page prefixes x 1 KV head x 1 and 3 row blocks; the 11- and 9-page
+    # prefixes of two sequences (16 rows): one wave item each
+    assert h[5] == 8 and h[4] == 3 * 1 + 4 * 3 and h[6] == 2
+    _check(run, got, run.reference(), "groups")
+
+
+@pytest.mark.parametrize("fmt", FORMATS, ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8"])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_cascade_formats(backend, fmt, d):
+    """A two-level tree (a root shared by every leaf, then pairs) in every
+    format and head_dim: group items read the root; f32 queries have none
+    (wave items only)."""
+    rng = np.random.default_rng(d + fmt[1])
+    perm = iter(rng.permutation(2048).tolist())
+    take = lambda n: [next(perm) for _ in range(n)]  # noqa: E731
+    root = take(37)
+    tables = []
+    for _ in range(6):
+        mid = root + take(9)
+        tables += [mid + take(1 + int(rng.integers(0, 4))) for _ in range(2)]
+    lpl = rng.integers(1, 17, len(tables)).astype(np.int32)
+    w = workloads.custom(tables, 16, 2, d, fmt[0], fmt[1], 2048, last_page_len=lpl)
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK
+    assert (_grouped(run) > 0) == (fmt[0] != _lib.DTYPE_F32)
+    _check(run, got, run.reference(), f"cascade d={d} {fmt}")
+
+
+def test_bad_id_in_a_shared_prefix_zeros_the_group(backend):
+    """A page id outside the pool inside a group's shared pages is in every
+    member's table: all members get zeros and the status DH_EINVAL; a bad id
+    in one member's own pages zeros that member only."""
+    rng = np.random.default_rng(9)
+    perm = iter(rng.permutation(1024).tolist())
+    take = lambda n: [next(perm) for _ in range(n)]  # noqa: E731
+    shared = take(16)
+    tables = [shared + take(2) for _ in range(4)] + [take(5)]
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 1024)
+    run = CsrRun(w, backend)
+    got, st = run.run()
+    assert st == _lib.DH_OK and _grouped(run) > 0
+    good = run.reference()
+    _check(run, got, good, "shared ok")
+    ix = w.indices.astype(np.int64).copy()
+    for b in range(4):
+        ix[w.indptr[b] + 5] = 5000                        # the same shared page in every member
+    got, st = run.run(indices=ix)
+    assert st == _lib.DH_EINVAL
+    assert np.all(got[:4] == 0)
+    _check(run, got[4:], good[4:], "bystander")
+    ix = w.indices.astype(np.int64).copy()
+    ix[w.indptr[2] + 16] = -3                             # member 2's own page
+    got, st = run.run(indices=ix)
+    assert st == _lib.DH_EINVAL
+    assert np.all(got[2] == 0)
+    keep = [0, 1, 3, 4]
+    _check(run, got[keep], good[keep], "one member bad")
 
 
 def test_empty_sequences_and_full_last_pages(backend):
@@ -185,12 +300,13 @@ def test_bad_ids_and_indptr_zero_their_sequences(backend):
 
 
 def test_tables_larger_than_the_workspace(backend):
-    """A workspace sized for a few pages holds batch + 1 chunk slots: tables
-    that need more chunks of 256 pages leave every output zero with status
-    DH_ENOMEM; a workspace below batch + 1 slots is refused on the host."""
+    """A workspace sized for one page holds a handful of chunk slots (batch
+    + 1, plus the cascade's allowance of one per sequence): tables that need
+    more chunks of 256 pages leave every output zero with status DH_ENOMEM;
+    a workspace below batch + 1 slots is refused on the host."""
     import torch
-    tables = [list(range(1, 600)), [700]]
-    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 1024)
+    tables = [list(range(1, 2400)), [2500]]
+    w = workloads.custom(tables, 8, 2, 64, _lib.DTYPE_BF16, _lib.KV_BF16, 4096)
     run = CsrRun(w, backend, ws_pages=1)
     got, st = run.run()
     assert st == _lib.DH_ENOMEM
