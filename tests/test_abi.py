@@ -181,10 +181,16 @@ def test_csr_workspace_size_grows_then_caps():
     sizes = [csr_workspace_size(cfg, 64, t) for t in (1, 8, 64, 512, 4096, 34304, 1 << 20, 1 << 24)]
     assert all(s > 0 and s % 256 == 0 for s in sizes)
     assert sizes == sorted(sizes)
-    assert sizes[-1] == sizes[-2] or sizes[-1] - sizes[-2] < sizes[-2]   # capped at 4096 extra slots
+    assert sizes[-1] == sizes[-2] or sizes[-1] - sizes[-2] < sizes[-2]   # capped slot counts
     assert csr_workspace_size(cfg, 65, 34304) > sizes[5]
-    # f32 queries keep fp32 partial states: larger
+    # f32 queries keep fp32 partial states: larger (one sequence: no cascade
+    # room for either)
     cfg32 = AttentionConfig(32, 8, 128)
     cfg32.q_dtype = _lib.DTYPE_F32
     cfg32.kv_format = _lib.KV_F32
-    assert csr_workspace_size(cfg32, 64, 34304) > sizes[5]
+    assert csr_workspace_size(cfg32, 1, 34304) > csr_workspace_size(cfg, 1, 34304)
+    # 16-bit queries over 2..512 sequences may find shared prefixes: room for
+    # their chunks (f32 queries never group, so their larger states do not
+    # make up for it here)
+    assert csr_workspace_size(cfg, 64, 34304) > csr_workspace_size(cfg32, 64, 34304)
+    assert csr_workspace_size(cfg, 513, 34304) < csr_workspace_size(cfg, 512, 34304)
