@@ -2729,6 +2729,7 @@ struct CsrCascade {
     uint32_t mn[kCsrCascadeMaxBatch];      // at a head: shortest common prefix of its run
     uint32_t skip[kCsrCascadeMaxBatch];    // skip word of b (AttendArgs::csr_skip)
     uint32_t ip[kCsrCascadeMaxBatch];      // indptr[b]
+    uint32_t ip_end;                       // indptr[batch]
     uint32_t lv[kCsrMaxLevels][kCsrCascadeMaxBatch];   // node id + 1 of b at a level | slot offset << 16
     uint32_t b0[kCsrMaxNodes], cnt[kCsrMaxNodes], npd[kCsrMaxNodes], len[kCsrMaxNodes];
     uint32_t gc[kCsrMaxNodes], kind[kCsrMaxNodes], item0[kCsrMaxNodes], ss0[kCsrMaxNodes];
@@ -2780,7 +2781,10 @@ __device__ uint32_t csr_cascade(const CsrPlanArgs& p, CsrCascade& c, uint32_t* s
         #pragma unroll
         for (uint32_t l = 0; l < kCsrMaxLevels; ++l) c.lv[l][b] = 0u;
     }
-    if (tid == 0) c.nn = 0;
+    if (tid == 0) {
+        c.nn = 0;
+        c.ip_end = uint32_t(p.indptr[B]);
+    }
     __syncthreads();
     auto internal = [&](uint32_t b) {
         return b > 0 && c.pd[b] != kCsrNoDepth && c.lcp[b] >= c.pd[b] + kCsrMinShared;
@@ -2951,54 +2955,19 @@ __device__ uint32_t csr_cascade(const CsrPlanArgs& p, CsrCascade& c, uint32_t* s
     return on ? ci : 0u;
 }
 
-// Items and seqslot entries of the cascade's nodes, one wave per node
-// (first slots of the sequences in c.tmp; seqslot entries from n_chunks on,
-// after the wave items' chunks).  Group items of a node cover unit u =
-// chunk * hkv + KV head and row block rb; units are taken eight at a time,
-// each with all its row blocks eight items apart, so the items reading the
-// same pages run on the same XCD (workgroup i runs on XCD i mod 8) and share
-// its L2.  Node wave items follow the group items in p.gitems.
-// Item i of a cascade node (CSR path): a group item (kind bit 0) of unit u
-// = chunk * hkv + KV head and row block rb, units eight at a time with
-// their row blocks eight items apart (items reading the same pages on one
-// XCD, workgroup i running on XCD i mod 8), or a wave item of 16 rows.
-__device__ __forceinline__ void csr_node_item(const CsrPlanArgs& p, uint32_t i, uint32_t b0, uint32_t cnt,
-                                                       uint32_t pd, uint32_t len, uint32_t g, uint32_t kind,
-                                                       uint32_t item0, uint32_t ss0, uint32_t p0, uint32_t n_chunks,
-                                                       uint32_t n_group, uint32_t gchunk) {
-    const uint32_t rows = cnt * p.r, GR = p.group_rows;
-    Item it;
-    if (kind & 1u) {
-        const uint32_t units = g * p.hkv, rbk = (rows + GR - 1) / GR;
-        const uint32_t blk = i / (8 * rbk), within = i - blk * 8 * rbk;
-        const uint32_t m = min(8u, units - blk * 8), rb = within / m, u = blk * 8 + within - rb * m;
-        const uint32_t chk = u / p.hkv;
-        it.page_off = p0 + pd + chk * gchunk;
-        it.npages = min(gchunk, len - pd - chk * gchunk);
-        it.seq_off = n_chunks + ss0 + chk * cnt;
-        it.row_begin = rb * GR;
-        it.nrows = min(GR, rows - rb * GR);
-        it.kv_head = u - chk * p.hkv;
-    } else {
-        const uint32_t nrb = (rows + kWaveRows - 1) / kWaveRows;
-        const uint32_t u = i / nrb, rb = i - u * nrb, chk = u / p.hkv;
-        it.page_off = p0 + pd + chk * kCsrWaveChunk;
-        it.npages = min(kCsrWaveChunk, len - pd - chk * kCsrWaveChunk);
-        it.seq_off = n_chunks + ss0 + chk * cnt;
-        it.row_begin = rb * kWaveRows;
-        it.nrows = min(uint32_t(kWaveRows), rows - rb * kWaveRows);
-        it.kv_head = u - chk * p.hkv;
-    }
-    it.flags = 0u;
-    it.tail_seq = b0;
-    p.gitems[((kind & 1u) ? 0u : n_group) + item0 + i] = it;
-}
-
+// Items and seqslot entries of the cascade's nodes (first slots of the
+// sequences in c.tmp; seqslot entries from n_chunks on, after the wave
+// items' chunks).  Group items of a node cover unit u = chunk * hkv + KV
+// head and row block rb; units are taken eight at a time, each with all its
+// row blocks eight items apart, so the items reading the same pages run on
+// the same XCD (workgroup i runs on XCD i mod 8) and share its L2.  A node's
+// wave items (16 rows each) go unit by unit, row blocks within; they follow
+// the group items in p.gitems.  red_scratch: the planning kernel's
+// reduction space.
 template <uint32_t NT>
 __device__ void csr_cascade_emit(const CsrPlanArgs& p, const CsrCascade& c, uint32_t n_chunks, uint32_t n_group,
-                                 uint32_t gchunk) {
-    constexpr uint32_t NW = NT / 64;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, GR = p.group_rows;
+                                 uint32_t gchunk, uint32_t* red_scratch) {
+    const uint32_t tid = threadIdx.x, GR = p.group_rows;
     // Seqslots, one thread per sequence: for each node of it (one a level),
     // its slot of every chunk (its first slot, the chunks of its shallower
     // nodes, then the chunk's index) at entry ss0 + chunk * cnt + member.
@@ -3013,71 +2982,108 @@ __device__ void csr_cascade_emit(const CsrPlanArgs& p, const CsrCascade& c, uint
             for (uint32_t chk = 0; chk < g; ++chk) dst[chk * cnt] = SeqSlot{b, s0 + chk};
         }
     }
-    // Items.  A node with at most 64 items is written by one thread alone
-    // (most nodes of a tree are small, and a thread per node keeps them in
-    // parallel); a larger one by a whole wave, from a list of them.
-    __shared__ uint32_t s_big[kCsrMaxNodes + 1];
-    if (tid == 0) s_big[kCsrMaxNodes] = 0u;
-    __syncthreads();
+    // Items: the nodes' items as one range in node order (node k's at
+    // s_ws[k] ..), cut into equal contiguous blocks, one a thread.  A thread
+    // finds its block's first node by bisection, then walks the nodes'
+    // item orders (csr_node_item's) with counters: one division each to
+    // start a node, none per item.
+    __shared__ uint32_t s_ws[kCsrMaxNodes + 1];
     auto n_items = [&](uint32_t k) {
         const uint32_t rows = c.cnt[k] * p.r;
         return c.gc[k] * p.hkv * ((c.kind[k] & 1u) ? (rows + GR - 1) / GR : (rows + kWaveRows - 1) / kWaveRows);
     };
-    for (uint32_t k = tid; k < c.nn; k += NT) {
-        const uint32_t n = n_items(k);
-        if (n > 64u) {
-            s_big[atomicAdd(&s_big[kCsrMaxNodes], 1u)] = k;
-            continue;
-        }
-        const uint32_t b0 = c.b0[k];
-        const uint32_t cnt = c.cnt[k], pd = c.npd[k], len = c.len[k], g = c.gc[k], kind = c.kind[k];
-        const uint32_t item0 = c.item0[k], ss0 = c.ss0[k], p0 = c.ip[b0];
-        // The order of csr_node_item, walked with counters instead of
-        // divisions: units (chunk, KV head) eight at a time, then row
-        // blocks, then the units of the eight (group items); units, then
-        // row blocks (wave items).
-        const uint32_t rows = cnt * p.r, grp = kind & 1u;
-        const uint32_t rbk = grp ? (rows + GR - 1) / GR : (rows + kWaveRows - 1) / kWaveRows;
-        const uint32_t RR = grp ? GR : uint32_t(kWaveRows), ch = grp ? gchunk : kCsrWaveChunk;
-        const uint32_t units = g * p.hkv, step = grp ? 8u : 1u;
-        Item* out = p.gitems + (grp ? 0u : n_group) + item0;
-        uint32_t chk0 = 0, h0 = 0;                 // unit u0 = chk0 * hkv + h0
-        for (uint32_t u0 = 0; u0 < units; u0 += step) {
-            const uint32_t m = min(step, units - u0);
-            for (uint32_t rb = 0; rb < rbk; ++rb) {
-                uint32_t chk = chk0, h = h0;
-                for (uint32_t uu = 0; uu < m; ++uu) {
-                    Item it;
-                    it.page_off = p0 + pd + chk * ch;
-                    it.npages = min(ch, len - pd - chk * ch);
-                    it.seq_off = n_chunks + ss0 + chk * cnt;
-                    it.row_begin = rb * RR;
-                    it.nrows = min(RR, rows - rb * RR);
-                    it.kv_head = h;
-                    it.flags = 0u;
-                    it.tail_seq = b0;
-                    *out++ = it;
-                    if (++h == p.hkv) {
-                        h = 0;
-                        ++chk;
-                    }
-                }
-            }
-            for (uint32_t uu = 0; uu < m; ++uu) {
-                if (++h0 == p.hkv) {
-                    h0 = 0;
-                    ++chk0;
-                }
-            }
-        }
+    uint32_t carry = 0;
+    for (uint32_t k0 = 0; k0 < c.nn; k0 += NT) {
+        const uint32_t k = k0 + tid;
+        const uint32_t v = k < c.nn ? n_items(k) : 0u;
+        uint32_t x = v, y = 0u, tx, ty;
+        block_incl_scan2<NT>(x, y, red_scratch, tx, ty);
+        if (k < c.nn) s_ws[k] = carry + x - v;
+        carry += tx;
     }
+    if (tid == 0) s_ws[c.nn] = carry;
     __syncthreads();
-    for (uint32_t t = wave; t < s_big[kCsrMaxNodes]; t += NW) {
-        const uint32_t k = s_big[t], n = n_items(k), b0 = c.b0[k];
-        const uint32_t cnt = c.cnt[k], pd = c.npd[k], len = c.len[k], g = c.gc[k], kind = c.kind[k];
-        const uint32_t item0 = c.item0[k], ss0 = c.ss0[k], p0 = c.ip[b0];
-        for (uint32_t i = lane; i < n; i += 64)
-            csr_node_item(p, i, b0, cnt, pd, len, g, kind, item0, ss0, p0, n_chunks, n_group, gchunk);
+    const uint32_t total = carry, per = (total + NT - 1) / NT;
+    uint32_t f = min(total, tid * per);
+    const uint32_t fend = min(total, f + per);
+    if (f < fend) {
+        uint32_t lo = 0, hi = c.nn;   // the last node starting at or before f
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (s_ws[mid] <= f) lo = mid;
+            else hi = mid;
+        }
+        for (uint32_t k = lo; f < fend; ++k) {
+            const uint32_t nk0 = s_ws[k], nk1 = s_ws[k + 1];
+            if (nk1 <= f) continue;   // an empty node
+            const uint32_t b0 = c.b0[k], cnt = c.cnt[k], pd = c.npd[k], len = c.len[k], g = c.gc[k];
+            const uint32_t grp = c.kind[k] & 1u, item0 = c.item0[k], ss0 = c.ss0[k], p0 = c.ip[b0];
+            const uint32_t rows = cnt * p.r;
+            const uint32_t rbk = grp ? (rows + GR - 1) / GR : (rows + kWaveRows - 1) / kWaveRows;
+            const uint32_t RR = grp ? GR : uint32_t(kWaveRows), ch = grp ? gchunk : kCsrWaveChunk;
+            const uint32_t units = g * p.hkv;
+            uint32_t i = f - nk0;
+            const uint32_t iend = min(fend, nk1) - nk0;
+            // Position of item i: group items take units eight at a time
+            // (blk), all row blocks of the eight (rb), then the unit within
+            // (uu of m); wave items a unit (blk) and its row blocks.
+            uint32_t blk, rb, uu, m;
+            if (grp) {
+                blk = i / (8 * rbk);
+                const uint32_t w = i - blk * 8 * rbk;
+                m = min(8u, units - blk * 8);
+                rb = w / m;
+                uu = w - rb * m;
+            } else {
+                blk = i / rbk;
+                rb = i - blk * rbk;
+                uu = 0;
+                m = 1;
+            }
+            const uint32_t u0 = grp ? blk * 8 : blk, u = u0 + uu;
+            uint32_t chk0 = u0 / p.hkv, h0 = u0 - chk0 * p.hkv;     // unit blk * 8 (group items)
+            uint32_t chk = u / p.hkv, h = u - chk * p.hkv;          // the item's unit
+            auto next_unit = [&](uint32_t& ck, uint32_t& hh) {
+                if (++hh == p.hkv) {
+                    hh = 0;
+                    ++ck;
+                }
+            };
+            Item* out = p.gitems + (grp ? 0u : n_group) + item0;
+            for (; i < iend; ++i) {
+                Item it;
+                it.page_off = p0 + pd + chk * ch;
+                it.npages = min(ch, len - pd - chk * ch);
+                it.seq_off = n_chunks + ss0 + chk * cnt;
+                it.row_begin = rb * RR;
+                it.nrows = min(RR, rows - rb * RR);
+                it.kv_head = h;
+                it.flags = 0u;
+                it.tail_seq = b0;
+                out[i] = it;
+                // the next item's position
+                if (grp) {
+                    next_unit(chk, h);
+                    if (++uu == m) {
+                        uu = 0;
+                        chk = chk0;
+                        h = h0;
+                        if (++rb == rbk) {
+                            rb = 0;
+                            for (uint32_t t = 0; t < m; ++t) next_unit(chk0, h0);
+                            chk = chk0;
+                            h = h0;
+                            ++blk;
+                            m = min(8u, units - min(units, blk * 8));
+                        }
+                    }
+                } else if (++rb == rbk) {
+                    rb = 0;
+                    next_unit(chk, h);
+                }
+            }
+            f = min(fend, nk1);
+        }
     }
 }
 
@@ -3129,7 +3135,9 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     auto load = [&](uint32_t b, bool& ok) -> uint32_t {
         ok = false;
         if (b >= p.batch) return 0u;
-        const int32_t p0 = p.indptr[b], p1 = p.indptr[b + 1];
+        // With a cascade indptr is in LDS already (no second round trip).
+        const int32_t p0 = casc ? int32_t(cc.ip[b]) : p.indptr[b];
+        const int32_t p1 = casc ? int32_t(b + 1 < p.batch ? cc.ip[b + 1] : cc.ip_end) : p.indptr[b + 1];
         ok = p0 >= 0 && p1 >= p0 && uint32_t(p1 - p0) <= kMaxSeqPages;
         if (!ok) return 0u;
         return uint32_t(p1 - p0) - (grouped ? (cc.skip[b] & 0xFFFFu) : 0u);
@@ -3308,7 +3316,7 @@ __global__ __launch_bounds__(NT) void csr_plan_kernel(CsrPlanArgs p) {
     const bool emit = grouped && !overflow;
     if (emit) {
         __syncthreads();   // first slots (cc.tmp) of every sequence
-        csr_cascade_emit<NT>(p, cc, n_chunks, n_gitems, gchunk);
+        csr_cascade_emit<NT>(p, cc, n_chunks, n_gitems, gchunk, red);
     }
     if (tid == 0) {
         const uint32_t slots = n_chunks + gslots;
