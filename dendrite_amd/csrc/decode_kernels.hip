@@ -1386,7 +1386,7 @@ __device__ __forceinline__ PairMask<RT> causal_mask(int t, const uint32_t (&lenr
 // pair p, and the PV MFMAs.  PART masks tokens past n0 / n1 (the item's
 // last pair only); the last pair has no next pair (NEXT false).  KS: the
 // pages' K scales ks0, ks1 multiply the scores (K was staged unscaled).
-template <int D, bool F16, int NRT, bool PART, bool NEXT, bool KS = false>
+template <int D, bool F16, int NRT, bool PART, bool NEXT, bool KS = false, bool PF16 = F16>
 __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMask<DmaCfg<D>::RT>& pm,
                                          const LdsBases<D>& lb,
                                          const u32x4 (&qB)[DmaCfg<D>::RT][D / 32], f4 (&sc)[DmaCfg<D>::RT][2],
@@ -1402,7 +1402,7 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
         else lm[rt] = dma_lane_max<RT, PART>(sc, rt, pm.s0[rt], pm.s1[rt], g);
         need |= lm[rt] > rm.thr[rt];
     }
-    if (__ballot(need)) dma_rescale<D, NRT, F16>(lm, rm, Lsum, O, f, finv);
+    if (__ballot(need)) dma_rescale<D, NRT, PF16>(lm, rm, Lsum, O, f, finv);
     // Branch-free from here, so the scheduler sees one region: LDS reads
     // first, then the score MFMAs of pair p + 1 interleaved with the
     // softmax of pair p (a wave overlaps some of its VALU work with MFMAs
@@ -1422,7 +1422,7 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
     u32x4 pB[RT];
     const float f0 = KS ? f * ks0 : f, f1 = KS ? f * ks1 : f;
     #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<F16>(sc[rt], f0, f1, rm.m[rt], Lsum[rt]);
+    for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<PF16>(sc[rt], f0, f1, rm.m[rt], Lsum[rt]);
     if constexpr (NEXT) {
         dma_score_mma<D, F16, NRT>(kop, qB, sc);
         #pragma unroll
@@ -1435,7 +1435,7 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
     #pragma unroll
     for (int e = 0; e < D / 16; ++e) {
         #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<F16>(vop[e], pB[rt], O[rt][e]);
+        for (int rt = 0; rt < NRT; ++rt) O[rt][e] = mma16v<PF16>(vop[e], pB[rt], O[rt][e]);
     }
 }
 
@@ -1846,7 +1846,7 @@ __device__ __forceinline__ void dma8_pair(const AttendArgs& a, const Item& it, u
 }
 
 // Converts raw slot rs into bf16 slot bs (the whole workgroup; tid < 256).
-template <int D, uint32_t KVF, bool H>
+template <int D, uint32_t KVF, bool HK, bool HV>
 __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_t bs, int tid) {
     using C8 = Dma8Cfg<D>;
     using C = DmaCfg<D>;
@@ -1865,24 +1865,29 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
         uint32_t out[16];
         if constexpr (KVF == KVF_MX) {
             const float sc = e8m0_to_float(scl[(page * 2 + plane) * C8::SREC + row * (D / 32) + col0 / 32]);
-            #pragma unroll
-            for (int w = 0; w < 8; ++w) e4m3x4_cvt<H>(wd[w], sc, out[2 * w], out[2 * w + 1]);
+            if (plane == 0) {
+                #pragma unroll
+                for (int w = 0; w < 8; ++w) e4m3x4_cvt<HK>(wd[w], sc, out[2 * w], out[2 * w + 1]);
+            } else {
+                #pragma unroll
+                for (int w = 0; w < 8; ++w) e4m3x4_cvt<HV>(wd[w], sc, out[2 * w], out[2 * w + 1]);
+            }
         } else if (plane == 0) {
             // K: the codes alone (exact in bf16); the block scale multiplies
             // the scores, so the attention scale does not amplify a rounding
             // of code * scale.  (plane is wave-uniform: a wave converts 2048
             // consecutive bytes, whole planes at head_dim 128 and 256.)
             #pragma unroll
-            for (int w = 0; w < 8; ++w) e4m3x4_cvt<H>(wd[w], 1.f, out[2 * w], out[2 * w + 1]);
+            for (int w = 0; w < 8; ++w) e4m3x4_cvt<HK>(wd[w], 1.f, out[2 * w], out[2 * w + 1]);
         } else {
-            // V: code * scale in f32, rounded once to bf16 (RNE).
+            // V: code * scale in f32, rounded once to bf16 or f16 (RNE).
             const float sc = *reinterpret_cast<const float*>(scl + 4 * (page * 2 + plane));
             #pragma unroll
             for (int w = 0; w < 8; ++w) {
                 const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], false);
                 const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(wd[w], true);
-                out[2 * w] = pack2(lo[0] * sc, lo[1] * sc, H);
-                out[2 * w + 1] = pack2(hi[0] * sc, hi[1] * sc, H);
+                out[2 * w] = pack2(lo[0] * sc, lo[1] * sc, HV);
+                out[2 * w + 1] = pack2(hi[0] * sc, hi[1] * sc, HV);
             }
         }
         uint8_t* rowp = bf + page * C::PAGE + plane * C::PLANE + row * C::RB;
@@ -1894,7 +1899,7 @@ __device__ __forceinline__ void dma8_convert(uint8_t* ring, uint32_t rs, uint32_
     }
 }
 
-template <int D, uint32_t KVF, bool F16, int NRT, bool TAIL, bool CAUSAL>
+template <int D, uint32_t KVF, bool F16, int NRT, bool TAIL, bool CAUSAL, bool PF16 = F16>
 __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                 uint8_t* ring, int tid, int wave, int g, int c,
                                                 const RowTargets<DmaCfg<D>::RT>& rtg, int last_len,
@@ -1955,7 +1960,7 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
     }
     wait_vmcnt_any((pro - 1) * C8::PER_PAIR);   // raw pair 0 has landed
     block_barrier();                             // query rows read; raw pair 0 visible
-    dma8_convert<D, KVF, F16>(ring, 0, 0, tid);
+    dma8_convert<D, KVF, F16, PF16>(ring, 0, 0, tid);
     block_barrier();
     f4 sc[RT][2];
     u32x4 vop[D / 16];
@@ -1981,20 +1986,20 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
             if (pi + P - 1 < npairs) dma8_pair<D, KVF>(a, it, nid0, nid1, src, raw_lds, ps == 0 ? P - 1 : ps - 1, wave);
             nid0 = page_id(2 * (pi + P));
             nid1 = page_id(2 * (pi + P) + 1);
-            dma8_convert<D, KVF, F16>(ring, psn, (j + 1) & 1, tid);
+            dma8_convert<D, KVF, F16, PF16>(ring, psn, (j + 1) & 1, tid);
             block_barrier();
             if constexpr (NRT > 0) {
                 float ks0 = 1.f, ks1 = 1.f;
                 if constexpr (KS) k_scales(ps, ks0, ks1);
                 const int t = CAUSAL ? int(lim.tok0 + 2 * kPageSize * pi) : 0;
                 if (CAUSAL && t + 2 * kPageSize > int(lim.lmin))
-                    dma_step<D, F16, NRT, true, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
-                                                            causal_mask<RT>(t, rtg.len, int(lim.lmax)), lb, qB, sc,
-                                                            vop, rm, Lsum, O, g, f, finv, ks0, ks1);
+                    dma_step<D, F16, NRT, true, true, KS, PF16>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                                                                  causal_mask<RT>(t, rtg.len, int(lim.lmax)), lb, qB,
+                                                                  sc, vop, rm, Lsum, O, g, f, finv, ks0, ks1);
                 else
-                    dma_step<D, F16, NRT, false, true, KS>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
-                                                             uniform_mask<RT>(kPageSize, kPageSize), lb, qB, sc,
-                                                             vop, rm, Lsum, O, g, f, finv, ks0, ks1);
+                    dma_step<D, F16, NRT, false, true, KS, PF16>(j * C8::BF_PAIR, ((j + 1) & 1) * C8::BF_PAIR,
+                                                                   uniform_mask<RT>(kPageSize, kPageSize), lb, qB,
+                                                                   sc, vop, rm, Lsum, O, g, f, finv, ks0, ks1);
             }
             ps = psn;
             psn = psn + 1 == P ? 0 : psn + 1;
@@ -2014,12 +2019,12 @@ __device__ __forceinline__ void dma8_group_loop(const AttendArgs& a, const Item&
         }
         float ks0 = 1.f, ks1 = 1.f;
         if constexpr (KS) k_scales(ps, ks0, ks1);
-        dma_step<D, F16, NRT, true, false, KS>((pl & 1) * C8::BF_PAIR, 0, pm, lb, qB, sc, vop, rm, Lsum, O, g,
-                                                f, finv, ks0, ks1);
+        dma_step<D, F16, NRT, true, false, KS, PF16>((pl & 1) * C8::BF_PAIR, 0, pm, lb, qB, sc, vop, rm, Lsum, O,
+                                                      g, f, finv, ks0, ks1);
     }
 }
 
-template <int D, uint32_t KVF, bool F16, int NRT, bool PF>
+template <int D, uint32_t KVF, bool F16, int NRT, bool PF, bool PF16 = F16>
 __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& it, const uint32_t* ids,
                                                uint8_t* ring, int tid, int wave, int g, int c,
                                                const RowTargets<DmaCfg<D>::RT>& rtg, int last_len) {
@@ -2039,18 +2044,53 @@ __device__ __forceinline__ void dma8_group_run(const AttendArgs& a, const Item& 
     }
     if constexpr (PF) {   // prefill plans: every item is causal
         const ItemLim lim = a.item_lim[blockIdx.x];
-        dma8_group_loop<D, KVF, F16, NRT, false, true>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm,
+        dma8_group_loop<D, KVF, F16, NRT, false, true, PF16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, lim, qB, rm,
                                                   L, O);
     } else if (it.flags & kItemTail) {
-        dma8_group_loop<D, KVF, F16, NRT, true, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+        dma8_group_loop<D, KVF, F16, NRT, true, false, PF16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                   qB, rm, L, O);
     } else {
-        dma8_group_loop<D, KVF, F16, NRT, false, false>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
+        dma8_group_loop<D, KVF, F16, NRT, false, false, PF16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len, ItemLim{},
                                                    qB, rm, L, O);
     }
     write_partial_dma<D, RT, PF>(a, it, wave, NRT, rtg, rm.m, L, O, g, c, F16);
 }
 
+// Whether the V values of KV head h in page `page` fit f16: FP8's
+// per-(page, head) scale at most 146 (448 x 146 < 65504), MXFP8's E8M0
+// exponents of the page's 16 tokens x D/32 groups at most 134 (448 x 2^7).
+// Smaller values only lose bits below f16's least subnormal, far under the
+// output tolerance.
+template <int D, uint32_t KVF>
+__device__ __forceinline__ bool v_fits_f16(const AttendArgs& a, uint32_t page, uint32_t h) {
+    const uint8_t* sc = static_cast<const uint8_t*>(a.scales);
+    if constexpr (KVF == KVF_FP8) {
+        const uint64_t rec = uint64_t(2) * a.hkv * 4;
+        const float s = *reinterpret_cast<const float*>(sc + page * rec + (a.hkv + h) * 4);
+        return s <= 146.f;   // NaN: false
+    } else {
+        constexpr int G = D / 32;
+        const uint64_t rec = uint64_t(2) * a.hkv * kPageSize * G;
+        const u32x4* p = reinterpret_cast<const u32x4*>(sc + page * rec + uint64_t(a.hkv + h) * kPageSize * G);
+        uint32_t big = 0;
+        #pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const u32x4 w = p[j];
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                #pragma unroll
+                for (int b = 0; b < 32; b += 8) big |= ((w[i] >> b) & 0xFFu) > 134u ? 1u : 0u;
+        }
+        return big == 0;
+    }
+}
+
+// 8-bit group item.  With bf16 queries the probabilities and V go into
+// the PV products as f16 when every V value of the item's pages fits f16
+// (checked on the scales with the page ids): bf16's 8-bit significand on
+// the probabilities was the largest error term at C5's shape (1.2e-2 beyond
+// the output rounding in an emulation of this arithmetic, 4e-3 with f16
+// probabilities in the shared-prefix items).  The scores stay bf16 x bf16.
 template <int D, uint32_t KVF, bool F16, bool PF>
 __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item& item, int tid, int wave, int g,
                                                 int c) {
@@ -2058,20 +2098,35 @@ __device__ __forceinline__ void group_item_dma8(const AttendArgs& a, const Item&
     using C8 = Dma8Cfg<D>;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[C8::LDS];
     __shared__ uint32_t ids[PF ? kPrefillMaxPages : kGroupMaxPages];
+    constexpr bool V16 = !F16 && !PF;   // probabilities may go f16
     const Item it = uniform_item(item);
     RowTargets<C::RT> rtg;
     dma_row_targets<D, C::RT>(a, it, wave, c, rtg);
     const int last_len = item_last_len(a, it);
+    int big = 0;
     for (uint32_t i = tid; i < it.npages; i += kWaves * 64) {
         const uint32_t pg = a.pages[it.page_off + i];
-        ids[i] = pg < a.page_limit ? pg : 0u;
+        const uint32_t id = pg < a.page_limit ? pg : 0u;
+        ids[i] = id;
+        if constexpr (V16) big |= v_fits_f16<D, KVF>(a, id, it.kv_head) ? 0 : 1;
     }
-    __syncthreads();
+    bool pf16 = false;
+    if constexpr (V16) pf16 = __syncthreads_or(big) == 0;
+    else __syncthreads();
     const int ntiles = int((it.nrows + kTileRows - 1) / kTileRows);
     const int nrt = ntiles > wave ? min(C::RT, (ntiles - wave + kWaves - 1) / kWaves) : 0;
-    if (nrt >= 2) dma8_group_run<D, KVF, F16, C::RT, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else if (nrt == 1) dma8_group_run<D, KVF, F16, 1, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
-    else dma8_group_run<D, KVF, F16, 0, PF>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    auto run = [&](auto pfI) {
+        constexpr bool P16 = decltype(pfI)::value != 0;
+        if (nrt >= 2) dma8_group_run<D, KVF, F16, C::RT, PF, P16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+        else if (nrt == 1) dma8_group_run<D, KVF, F16, 1, PF, P16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+        else dma8_group_run<D, KVF, F16, 0, PF, P16>(a, it, ids, ring, tid, wave, g, c, rtg, last_len);
+    };
+    if constexpr (V16) {
+        if (pf16) run(Idx<1>{});
+        else run(Idx<0>{});
+    } else {
+        run(Idx<F16 ? 1 : 0>{});
+    }
 }
 
 // ---------------------------------------------------------------- attend16

@@ -25,7 +25,7 @@ constexpr int kPageSize = 16;       // tokens per page (dendrite-ffi flashinfer/
 constexpr int kWaves = 4;           // wave64s per workgroup
 constexpr int kTileRows = 16;       // query rows of one MFMA tile
 constexpr int kWaveRows = 16;       // rows of a wave item: one tile, one wave
-constexpr int kGroupMaxPages = 256; // pages of one group item (LDS page-id list)
+constexpr int kGroupMaxPages = 512; // pages of one group item (LDS page-id list)
 constexpr int kPrefillMaxPages = 2048;  // pages of one prefill item (its LDS page-id list)
 constexpr int kWaveIdRegs = 4;      // wave items hold <= 256 page ids in registers
 // Row tiles per wave of a group item: pages staged by direct global->LDS

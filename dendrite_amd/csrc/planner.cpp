@@ -574,9 +574,9 @@ int build_plan(const PlanInput& in, HostPlan& out, std::string& err) {
     }
     out.num_group_items = uint32_t(gorder.size());
     out.num_wave_items = uint32_t(waves.size() + direct_tasks.size() * kWaves);
-    for (const Item& it : out.items)
-        if (it.npages > kMaxItemPages) {
-            err = "internal: an item of " + std::to_string(it.npages) + " pages";
+    for (size_t i = 0; i < out.items.size(); ++i)
+        if (out.items[i].npages > (i < out.num_group_items ? uint32_t(kGroupMaxPages) : kMaxItemPages)) {
+            err = "internal: an item of " + std::to_string(out.items[i].npages) + " pages";
             return DH_EINVAL;
         }
     // The items of each sequence's last chunk, by final item index.

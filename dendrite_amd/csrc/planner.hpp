@@ -8,9 +8,9 @@
 namespace dh {
 
 // Pages reserved after each sequence's last chunk, so a decode plan can take
-// that many appended pages in place; no item holds more than kMaxItemPages
-// (a wave item keeps its page ids in registers, four per lane; a group item
-// in a 256-entry LDS list).
+// that many appended pages in place; no wave item holds more than
+// kMaxItemPages (it keeps its page ids in registers, four per lane), no group
+// item more than kGroupMaxPages (its LDS page-id list).
 constexpr uint32_t kTailSlack = 16;
 constexpr uint32_t kMaxItemPages = 256;
 
