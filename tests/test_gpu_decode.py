@@ -150,6 +150,41 @@ def test_scores_rising_late(backend, shape, fmt):
     assert err <= TOL[w.q_dtype], err
 
 
+@pytest.mark.parametrize("kvf", [_lib.KV_FP8_E4M3, _lib.KV_MXFP8], ids=["fp8", "mxfp8"])
+def test_v_beyond_f16_keeps_bf16_probabilities(backend, kvf):
+    """bf16 queries over 8-bit pools: shared-prefix items take f16
+    probabilities and V only when every V value of their pages fits f16.
+    Here some prefix pages' V scales put values past 65 504 (FP8 scale x 1e5,
+    MXFP8 exponents + 17): the items holding them keep bf16 and stay finite
+    (f16 would overflow to inf), within bf16's relative error of the
+    largest output; the other items use f16."""
+    prefix = list(range(10, 42))
+    tables = [prefix + [60 + i] for i in range(6)]
+    w = workloads.custom(tables, 64, 8, 128, _lib.DTYPE_BF16, kvf, 128, last_page_len=[7] * 6, name="vbig")
+    run = GpuRun(w, backend, shared_chunk_pages=8)
+    big = np.isin(run.ids, prefix[4:6])
+    if kvf == _lib.KV_FP8_E4M3:
+        sc = run.scales.view(np.float32).reshape(len(run.ids), 2, w.hkv)
+        sc[big, 1] *= 1.0e5
+        assert sc[big, 1].min() > 146.0                        # 448 x scale past f16's 65 504
+    else:
+        sc = run.scales.reshape(len(run.ids), 2, w.hkv, 16, w.d // 32)
+        sc[big, 1] = np.minimum(sc[big, 1].astype(np.int32) + 17, 254).astype(np.uint8)
+        assert sc[big, 1].max() > 134                           # 448 x 2^7 is the last that fits
+    run.pool.write_pages(run.ids, run.data, run.scales)
+    assert run.plan.stats()["num_group_items"] > 0
+    got = run.run()
+    ref = run.reference()
+    rel = max_abs_err(got, ref) / np.abs(ref).max()
+    print(f"[case] vbig kvf={kvf}: max |ref| {np.abs(ref).max():.3e}, max abs err relative to it {rel:.3e}",
+          flush=True)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    # Values this large are outside what the absolute 2e-2 bar is stated
+    # for (bf16 probabilities alone move outputs of 1e4 by tens); relative
+    # to the largest output the error is that of bf16 weights.
+    assert rel <= 1e-2, rel
+
+
 @pytest.mark.parametrize("fmt", FORMATS + FORMATS_F16Q,
                          ids=["bf16", "f16", "f32", "fp8", "mxfp8", "f16q-fp8", "f16q-mxfp8"])
 @pytest.mark.parametrize("shape", [(32, 4, 64), (32, 8, 128), (16, 2, 256), (16, 1, 64), (64, 2, 128),
