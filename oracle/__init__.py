@@ -29,7 +29,7 @@ INVALID = 0xFFFFFFFF
 def build() -> str:
     """Compile oracle.c with gcc (OpenMP) into oracle/liboracle.so."""
     tmp = LIB_PATH + ".tmp"
-    subprocess.run(["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-Wall", SOURCE, "-o", tmp, "-lm"],
+    subprocess.run(["gcc", "-O3", "-fopenmp", "-fPIC", "-shared", "-Wall", SOURCE, "-o", tmp, "-lm"],
                    check=True, capture_output=True, text=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH

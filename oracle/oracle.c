@@ -62,6 +62,16 @@ double oracle_e4m3(uint8_t b) {
 /* OCP MX E8M0: 2^(e - 127), e = 255 is NaN. */
 double oracle_e8m0(uint8_t e) { return e == 255 ? NAN : ldexp(1.0, (int)e - 127); }
 
+/* Both decodings for every byte, filled when the library loads, so the
+ * element reads below look values up instead of recomputing them. */
+static double dec_e4m3[256], dec_e8m0[256];
+__attribute__((constructor)) static void fill_decode_tables(void) {
+    for (int c = 0; c < 256; ++c) {
+        dec_e4m3[c] = oracle_e4m3((uint8_t)c);
+        dec_e8m0[c] = oracle_e8m0((uint8_t)c);
+    }
+}
+
 /* ------------------------------------------------ quantise-on-write oracle
  * The page write rule (dh_pool_write_pages_device), restated from the format
  * definitions: E4M3 "FN" encodes a float as the nearest finite code value
@@ -223,13 +233,13 @@ static double kv_elem(const pool_view* pv, uint32_t row, uint32_t plane, uint32_
         case FP8: {
             float sc;
             memcpy(&sc, pv->scales + (size_t)row * pv->scale_bytes + ((size_t)plane * pv->hkv + head) * 4, 4);
-            return oracle_e4m3(p[idx]) * (double)sc;
+            return dec_e4m3[p[idx]] * (double)sc;
         }
         default: {
             const uint32_t G = pv->d / 32;
             const uint8_t e = pv->scales[(size_t)row * pv->scale_bytes +
                                          (((size_t)plane * pv->hkv + head) * OR_PAGE + tok) * G + dim / 32];
-            return oracle_e4m3(p[idx]) * oracle_e8m0(e);
+            return dec_e4m3[p[idx]] * dec_e8m0[e];
         }
     }
 }
@@ -292,33 +302,64 @@ int oracle_decode(const void* data, const void* scales, const uint32_t* page_map
         int T = 0;
         for (int i = 0; i < n; ++i) T += ntok[i];
         double* s = (double*)malloc(((size_t)T + 1) * sizeof(double));
-        for (uint32_t h = 0; h < hq; ++h) {
-            double* o = out + ((size_t)si * hq + h) * d;
-            memset(o, 0, d * sizeof(double));
-            if (T == 0) continue;
-            const uint32_t kh = kv_head_of(h, hq, hkv, gqa);
-            const size_t qb = ((size_t)b * hq + h) * d;
+        /* K and V of one KV head, dequantised once for the query heads that
+         * share it (the same values kv_elem gives, in token order). */
+        double* kd = (double*)malloc(((size_t)T * d + 1) * sizeof(double));
+        double* vd = (double*)malloc(((size_t)T * d + 1) * sizeof(double));
+        double* qd = (double*)malloc((size_t)d * sizeof(double));
+        for (uint32_t kh = 0; kh < hkv; ++kh) {
             int t = 0;
-            double mx = -INFINITY;
             for (int i = 0; i < n; ++i)
-                for (int j = 0; j < ntok[i]; ++j, ++t) {
+                for (int j = 0; j < ntok[i]; ++j, ++t)
+                    for (uint32_t k = 0; k < d; ++k) {
+                        kd[(size_t)t * d + k] = kv_elem(&pv, rows[i], 0, kh, j, k);
+                        vd[(size_t)t * d + k] = kv_elem(&pv, rows[i], 1, kh, j, k);
+                    }
+            for (uint32_t h = 0; h < hq; ++h) {
+                if (kv_head_of(h, hq, hkv, gqa) != kh) continue;
+                double* o = out + ((size_t)si * hq + h) * d;
+                memset(o, 0, d * sizeof(double));
+                if (T == 0) continue;
+                const size_t qb = ((size_t)b * hq + h) * d;
+                double mx = -INFINITY;
+                for (uint32_t k = 0; k < d; ++k) qd[k] = q_elem(q, q_dtype, qb + k);
+                /* four tokens' dot products side by side, each summed over
+                 * k in order (the same sums as one token at a time) */
+                for (t = 0; t + 4 <= T; t += 4) {
+                    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+                    const double* k0 = kd + (size_t)t * d;
+                    for (uint32_t k = 0; k < d; ++k) {
+                        a0 += qd[k] * k0[k];
+                        a1 += qd[k] * k0[d + k];
+                        a2 += qd[k] * k0[2 * d + k];
+                        a3 += qd[k] * k0[3 * d + k];
+                    }
+                    s[t] = a0 * (double)scale;
+                    s[t + 1] = a1 * (double)scale;
+                    s[t + 2] = a2 * (double)scale;
+                    s[t + 3] = a3 * (double)scale;
+                }
+                for (; t < T; ++t) {
                     double acc = 0.0;
-                    for (uint32_t k = 0; k < d; ++k) acc += q_elem(q, q_dtype, qb + k) * kv_elem(&pv, rows[i], 0, kh, j, k);
+                    for (uint32_t k = 0; k < d; ++k) acc += qd[k] * kd[(size_t)t * d + k];
                     s[t] = acc * (double)scale;
+                }
+                for (t = 0; t < T; ++t)
                     if (s[t] > mx) mx = s[t];
+                double den = 0.0;
+                for (t = 0; t < T; ++t) {
+                    s[t] = exp(s[t] - mx);
+                    den += s[t];
                 }
-            double den = 0.0;
-            for (t = 0; t < T; ++t) {
-                s[t] = exp(s[t] - mx);
-                den += s[t];
-            }
-            t = 0;
-            for (int i = 0; i < n; ++i)
-                for (int j = 0; j < ntok[i]; ++j, ++t) {
+                for (t = 0; t < T; ++t) {
                     const double w = s[t] / den;
-                    for (uint32_t k = 0; k < d; ++k) o[k] += w * kv_elem(&pv, rows[i], 1, kh, j, k);
+                    for (uint32_t k = 0; k < d; ++k) o[k] += w * vd[(size_t)t * d + k];
                 }
+            }
         }
+        free(kd);
+        free(vd);
+        free(qd);
         free(s);
         free(rows);
         free(ntok);
