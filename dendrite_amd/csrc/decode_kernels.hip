@@ -1403,19 +1403,13 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
         need |= lm[rt] > rm.thr[rt];
     }
     if (__ballot(need)) dma_rescale<D, NRT, PF16>(lm, rm, Lsum, O, f, finv);
-    // Branch-free from here, so the scheduler sees one region: LDS reads
-    // first, then the score MFMAs of pair p + 1 interleaved with the
-    // softmax of pair p (a wave overlaps some of its VALU work with MFMAs
-    // in flight), then the PV MFMAs.
+    // Branch-free from here, so the scheduler sees one region, in this
+    // order (pinned: a wave issues in order, and at most 15 LDS reads may
+    // be outstanding before issue stalls): the K reads of pair p + 1; the
+    // softmax of pair p (VALU), which needs no LDS, while they are in
+    // flight; the score MFMAs of pair p + 1 with the V reads of pair p
+    // issued one between each two; then the PV MFMAs of pair p.
     __builtin_amdgcn_sched_barrier(0);
-    dma_v_operands<D>(vs, lb, vop);
-    if constexpr (PART) {
-        #pragma unroll
-        for (int e = 0; e < D / 16; ++e) {
-            mask_v_tr(vop[e], 0, g, pm.v0);
-            mask_v_tr(vop[e], 2, g, pm.v1);
-        }
-    }
     u32x4 kop[2][KB];
     if constexpr (NEXT) dma_k_operands<D>(ks, lb, kop);
     __builtin_amdgcn_sched_barrier(0);
@@ -1423,15 +1417,25 @@ __device__ __forceinline__ void dma_step(uint32_t vs, uint32_t ks, const PairMas
     const float f0 = KS ? f * ks0 : f, f1 = KS ? f * ks1 : f;
     #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) pB[rt] = dma_probs<PF16>(sc[rt], f0, f1, rm.m[rt], Lsum[rt]);
+    __builtin_amdgcn_sched_barrier(0);
+    dma_v_operands<D>(vs, lb, vop);
     if constexpr (NEXT) {
         dma_score_mma<D, F16, NRT>(kop, qB, sc);
+        constexpr int NM = NRT * 2 * KB, NV = D / 8;   // score MFMAs, V reads
         #pragma unroll
-        for (int k = 0; k < NRT * 2 * KB; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+        for (int k = 0; k < (NM > NV ? NM : NV); ++k) {
+            if (k < NV) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+            if (k < NM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PART) {
+        #pragma unroll
+        for (int e = 0; e < D / 16; ++e) {
+            mask_v_tr(vop[e], 0, g, pm.v0);
+            mask_v_tr(vop[e], 2, g, pm.v1);
+        }
+    }
     #pragma unroll
     for (int e = 0; e < D / 16; ++e) {
         #pragma unroll
